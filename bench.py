@@ -1,0 +1,225 @@
+"""Prefill throughput of the GPT-2 forward hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload gpt2|medium]
+
+Workload (default): GPT-2 124M architecture (12 layers, 12 heads, d 768, MLP 3072,
+vocab 50257), bf16 random-init weights N(0, 0.02) written as an HF GPT-2
+checkpoint directory and loaded through ``CutileGPT.load_from_huggingface``;
+uniform random token ids; one step = one prefill forward of batch 16 x seq 1024
+(16384 tokens) producing fp32 logits.  Inputs are resident on the GPU before
+the timed region.  Prints one JSON line.
+
+``roofline`` is the LM-head GEMM launch (the single largest launch: 2*16384*768*
+50257 FLOP), timed with stream events around that launch inside the timed
+steps.  ``cpu_baseline`` is the CPU oracle's fp32 forward of the same model
+(a minGPT-architecture PyTorch forward) on the host cores, over a bounded
+sample.  ``breakdown`` comes from one extra, separately timed forward with
+events around every launch.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import tempfile
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+WORKLOADS = {
+    "gpt2": dict(n_layer=12, n_head=12, n_embd=768, batch=16, seq=1024,
+                 name="gpt2-124m prefill b16xs1024"),
+    "medium": dict(n_layer=8, n_head=8, n_embd=512, batch=16, seq=256,
+                   name="medium-8L-512 prefill b16xs256"),
+}
+
+
+def flops(L, D, B, T, V=50257):
+    M = B * T
+    gemm = L * 2 * M * D * (3 * D + D + 4 * D + 4 * D)
+    head = 2 * M * D * V
+    attn = L * 4 * B * D * T * (T + 1) // 2  # causal half incl. diagonal, all heads
+    return gemm, head, attn
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="gpt2", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seqs", type=int, default=2,
+                    help="sequences (of seq_len tokens) per timed CPU-baseline forward")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build measures one GPU only (every box has a single MI355X); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from cutilegpt_amd import CutileGPT, GPTConfig
+    from cutilegpt_amd.hf_loader import save_hf_checkpoint
+
+    wl = WORKLOADS[args.workload]
+    L, H, D, B, T = wl["n_layer"], wl["n_head"], wl["n_embd"], wl["batch"], wl["seq"]
+    V = 50257
+    cfg = GPTConfig(vocab_size=V, block_size=1024, n_layer=L, n_head=H, n_embd=D)
+    dev = torch.device("cuda:0")
+
+    # bf16 N(0, 0.02) weights (biases 0, LN 1/0) through the HF checkpoint loader.
+    g = torch.Generator().manual_seed(0)
+    w = {}
+    bf = torch.bfloat16
+    rn = lambda *s: (torch.randn(*s, generator=g) * 0.02).to(bf)
+    w["wte"], w["wpe"] = rn(V, D), rn(1024, D)
+    for i in range(L):
+        p = f"h.{i}."
+        w[p + "ln_1.weight"], w[p + "ln_1.bias"] = torch.ones(D, dtype=bf), torch.zeros(D, dtype=bf)
+        w[p + "attn.c_attn.weight"], w[p + "attn.c_attn.bias"] = rn(3 * D, D), torch.zeros(3 * D, dtype=bf)
+        w[p + "attn.c_proj.weight"], w[p + "attn.c_proj.bias"] = rn(D, D), torch.zeros(D, dtype=bf)
+        w[p + "ln_2.weight"], w[p + "ln_2.bias"] = torch.ones(D, dtype=bf), torch.zeros(D, dtype=bf)
+        w[p + "mlp.c_fc.weight"], w[p + "mlp.c_fc.bias"] = rn(4 * D, D), torch.zeros(4 * D, dtype=bf)
+        w[p + "mlp.c_proj.weight"], w[p + "mlp.c_proj.bias"] = rn(D, 4 * D), torch.zeros(D, dtype=bf)
+    w["ln_f.weight"], w["ln_f.bias"] = torch.ones(D, dtype=bf), torch.zeros(D, dtype=bf)
+    w["lm_head.weight"] = w["wte"]
+    model = CutileGPT(cfg, dtype=bf, seed=0)
+    with tempfile.TemporaryDirectory() as ckpt:
+        save_hf_checkpoint(ckpt, w, cfg)
+        model.load_from_huggingface(ckpt)
+    ids = torch.randint(0, V, (B, T), generator=torch.Generator().manual_seed(1)).to(dev)
+    print(f"[bench] workload {wl['name']}: warmup {args.warmup}, steps {args.steps}",
+          file=sys.stderr, flush=True)
+
+    for _ in range(args.warmup):
+        model(ids)
+    torch.cuda.synchronize()
+
+    # Timed region: K forwards; events around the LM-head launch only.
+    stream = torch.cuda.current_stream()
+    head_ev = []
+
+    def head_probe(tag, start):
+        if tag == "lm_head":
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record(stream)
+            head_ev.append(ev)
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        model.forward(ids, probe=head_probe)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    head_ms = [head_ev[2 * i].elapsed_time(head_ev[2 * i + 1]) for i in range(args.steps)]
+    head_avg_ms = sum(head_ms) / len(head_ms)
+    ms_per_step = elapsed * 1e3 / args.steps
+    tokens = B * T
+    tok_s = tokens * args.steps / elapsed
+    gemm_f, head_f, attn_f = flops(L, D, B, T, V)
+    head_tflops = head_f / (head_avg_ms * 1e-3) / 1e12
+
+    # Breakdown: one more forward, events around every launch.
+    marks = []
+
+    def all_probe(tag, start):
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record(stream)
+        marks.append((tag, start, ev))
+
+    model.forward(ids, probe=all_probe)
+    torch.cuda.synchronize()
+    per = {}
+    for i in range(0, len(marks), 2):
+        tag, _, e0 = marks[i]
+        per.setdefault(tag, [0.0, 0])
+        per[tag][0] += e0.elapsed_time(marks[i + 1][2])
+        per[tag][1] += 1
+    M = B * T
+    work = {  # algorithmic FLOP (GEMM/attention) or bytes (LN/embedding) per forward
+        "gemm_qkv": ("TFLOP/s", L * 2 * M * D * 3 * D),
+        "gemm_proj": ("TFLOP/s", L * 2 * M * D * D),
+        "gemm_fc_gelu": ("TFLOP/s", L * 2 * M * D * 4 * D),
+        "gemm_mlp_proj": ("TFLOP/s", L * 2 * M * 4 * D * D),
+        "lm_head": ("TFLOP/s", head_f),
+        "attention": ("TFLOP/s", attn_f),
+        # add+LN: read x fp32 + delta bf16, write x fp32 + y bf16 (first: read x, write y)
+        "ln": ("GB/s", (2 * L) * M * D * (4 + 2 + 4 + 2) + M * D * (4 + 2)),
+        # gather: read wte + wpe rows bf16, write x fp32
+        "embedding": ("GB/s", M * D * (2 + 2 + 4)),
+    }
+    breakdown = {}
+    for tag, (ms, n) in per.items():
+        unit, amount = work[tag]
+        rate = amount / (ms * 1e-3) / (1e12 if unit == "TFLOP/s" else 1e9)
+        peak = PEAK_BF16_TFLOPS if unit == "TFLOP/s" else PEAK_HBM_GBS
+        breakdown[tag] = {"ms": round(ms, 4), "launches": n, unit: round(rate, 1),
+                          "frac": round(rate / peak, 4)}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(w, ids, H, args.cpu_seqs)
+
+    line = {
+        "metric": "prefill tok/s (GPT-2 124M, b16×s1024, bf16) + % of MFMA/HBM roofline",
+        "value": round(tok_s, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random N(0,0.02) bf16 weights via HF-format checkpoint, uniform ids)",
+        "config": {"workload": wl["name"], "n_layer": L, "n_head": H, "n_embd": D,
+                   "vocab_size": V, "batch": B, "seq_len": T, "logits": "fp32",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": "lm_head GEMM (gemm_kernel bf16, N=50257, K=768)",
+                     "achieved": round(head_tflops, 1), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(head_tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None, "avg_launch_ms": round(head_avg_ms, 4)},
+        "forward_tflops": round((gemm_f + head_f + attn_f) / (ms_per_step * 1e-3) / 1e12, 1),
+        "breakdown": breakdown,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(w, ids, n_head, n_seqs):
+    """CPU oracle fp32 forward (minGPT-architecture PyTorch) on the host cores:
+    1 warmup + 3 timed forwards of ``n_seqs`` sequences, median."""
+    import torch
+    from oracle import gpt_ref as R
+
+    threads = torch.get_num_threads()
+    w32 = {k: v.float() for k, v in w.items()}
+    w32["lm_head.weight"] = w32["wte"]
+    x = ids[:n_seqs].cpu()
+    times = []
+    with torch.inference_mode():
+        R.gpt_forward(w32, x, n_head, R.FLOWS["fp32"])
+        for _ in range(3):
+            t0 = time.perf_counter()
+            R.gpt_forward(w32, x, n_head, R.FLOWS["fp32"])
+            times.append(time.perf_counter() - t0)
+    med = sorted(times)[1]
+    return {"value": round(x.numel() / med, 1), "unit": "tok/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{n_seqs} x {x.shape[1]} tokens per forward, fp32, 1 warmup + 3 timed, median "
+                      f"{med:.2f} s (oracle.gpt_ref.gpt_forward, torch threads={threads}, "
+                      f"os.cpu_count()={os.cpu_count()})"}
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,386 @@
+// Causal flash attention forward on CDNA4 matrix cores.
+//
+// Work decomposition
+//  * One block = 4 wavefronts = BQ = 128 queries of one (batch, head); each wave
+//    owns QT = 2 sub-tiles of 16 queries.  Blocks are ordered so that the last
+//    (most expensive, under the causal mask) query blocks are dispatched first.
+//  * Keys/values stream through LDS in BKV = 64-row blocks, double-buffered
+//    through registers (the loads of block j+1 are in flight while block j is
+//    computed).  Under the causal mask the loop stops at the block holding the
+//    block's last query (causal tile skip) and only blocks that straddle the
+//    diagonal (or the end of the sequence) evaluate the mask.
+//
+// Matrix-core formulation (16x16 MFMA tiles, fp32 accumulation)
+//  * S^T = K Q^T: the K fragment is the MFMA "A" operand and the Q fragment the
+//    "B" operand, so lane l holds S^T[key = 4(l/16) + r][query = l%16]: every
+//    lane owns exactly one query.  The row maximum then needs two cross-lane
+//    shuffles (lanes l^16, l^32), and the running max, the normaliser and the
+//    rescale factor are per-lane scalars.
+//  * O^T = V^T P^T: V is stored transposed in LDS ([d][key], keys contiguous);
+//    the P operand is taken straight from the S^T accumulator registers.  The
+//    key order inside one MFMA k-slab is permuted identically on both operands
+//    (lane group g, element i <-> key 4g + i of the first 16-key tile, then of
+//    the second), which leaves the contraction unchanged.
+//  * bf16: v_mfma_f32_16x16x32_bf16; P is rounded to bf16 before P.V while the
+//    normaliser accumulates the unrounded fp32 P.  fp32: v_mfma_f32_16x16x4_f32.
+//  * Softmax runs in the base-2 domain with scale * log2(e) folded into one
+//    multiply; fully masked rows never produce NaN (the running max is clamped
+//    to 0 while it is still -inf).
+#include "common.h"
+
+namespace cgpt {
+
+constexpr int kAttnThreads = 256;
+constexpr int kAttnQT = 2;                         // 16-query sub-tiles per wave
+constexpr int kAttnBQ = 4 * 16 * kAttnQT;          // queries per block
+constexpr int kAttnBKV = 64;                       // keys per LDS block
+
+template <typename T> struct AttnMfma;
+template <> struct AttnMfma<bf16_t> {
+  __device__ static void run(const u32x4_t& a, const u32x4_t& b, f32x4_t& c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+};
+template <> struct AttnMfma<float> {
+  __device__ static void run(const u32x4_t& a, const u32x4_t& b, f32x4_t& c) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[j]), __uint_as_float(b[j]), c, 0,
+                                               0, 0);
+  }
+};
+
+__device__ __forceinline__ void store4_o(float* p, const float* v) { store_vec(p, v); }
+__device__ __forceinline__ void store4_o(bf16_t* p, const float* v) {
+  u32x2_t u = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  *reinterpret_cast<u32x2_t*>(p) = u;
+}
+
+template <typename T, int HD>
+__global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
+    const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V, T* __restrict__ O,
+    int H, int Tq, int Tk, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh,
+    int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t o_sb, int64_t o_sh,
+    int64_t o_st, float scale_log2, int causal, int n_bh) {
+  constexpr int QT = kAttnQT, BQ = kAttnBQ, BKV = kAttnBKV;
+  constexpr int EPC = 16 / sizeof(T);          // elements per 16-byte chunk
+  constexpr int CPR = HD / EPC;                // 16-byte chunks per K row
+  constexpr int SWZ = (CPR < 8 ? CPR : 8) - 1; // chunk swizzle mask
+  constexpr int KSTEP = 4 * EPC;               // head_dim covered by one k-slab
+  constexpr int NKS = (HD + KSTEP - 1) / KSTEP;
+  constexpr int ND = HD / 16;                  // 16-wide d tiles of O
+  constexpr int KROW = HD * static_cast<int>(sizeof(T));
+  // V^T rows are padded (8 B for bf16, 16 B for fp32) so the transposing writes
+  // of one wave spread over the LDS banks; reads stay 8/16-byte aligned.
+  constexpr int VROW = BKV * static_cast<int>(sizeof(T)) + (sizeof(T) == 2 ? 8 : 16);
+  constexpr int KBYTES = BKV * KROW;
+  constexpr int STAGE = KBYTES + HD * VROW;
+  constexpr int KCH = BKV * CPR;               // K chunks per block
+  constexpr int KL = (KCH + kAttnThreads - 1) / kAttnThreads;
+  constexpr int VCH = (BKV / 2) * CPR;         // (key pair, chunk) items per block
+  constexpr int VL = (VCH + kAttnThreads - 1) / kAttnThreads;
+  static_assert(HD % 16 == 0, "head_dim must be a multiple of 16");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, frow = lane & 15;
+
+  const int n_qblk = (Tq + BQ - 1) / BQ;
+  const int qb = n_qblk - 1 - static_cast<int>(blockIdx.x) / n_bh;  // heavy blocks first
+  const int bh = static_cast<int>(blockIdx.x) % n_bh;
+  const int b = bh / H, h = bh % H;
+  const int q0 = qb * BQ;
+  const int off = Tk - Tq;  // absolute position of query 0
+
+  const T* Qb = Q + b * q_sb + h * q_sh;
+  const T* Kb = K + b * k_sb + h * k_sh;
+  const T* Vb = V + b * v_sb + h * v_sh;
+
+  // Q fragments stay in registers for the whole key loop.
+  u32x4_t qf[QT][NKS];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int qi = q0 + wave * 16 * QT + qt * 16 + frow;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int c = 4 * ks + g;
+      qf[qt][ks] = (qi < Tq && c < CPR)
+                       ? *reinterpret_cast<const u32x4_t*>(Qb + qi * q_st + c * EPC)
+                       : u32x4_t{0, 0, 0, 0};
+    }
+  }
+
+  // Key range this block needs.
+  const int last_q = min(q0 + BQ, Tq) - 1 + off;  // absolute position of the block's last query
+  const int kv_end = causal ? min(last_q + 1, Tk) : Tk;
+  const int n_kv = (kv_end + BKV - 1) / BKV;
+  const int wave_q0 = q0 + wave * 16 * QT;
+  const int wave_last = min(wave_q0 + 16 * QT, Tq) - 1 + off;  // wave's last query position
+  const bool wave_live = wave_q0 < Tq;
+
+  u32x4_t rk[KL];
+  u32x4_t rv[VL][2];
+  auto gload = [&](int j) {
+    const int kv0 = j * BKV;
+#pragma unroll
+    for (int i = 0; i < KL; ++i) {
+      const int item = tid + i * kAttnThreads;
+      if (item < KCH) {
+        const int key = min(kv0 + item / CPR, Tk - 1);
+        rk[i] = *reinterpret_cast<const u32x4_t*>(Kb + key * k_st + (item % CPR) * EPC);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VL; ++i) {
+      const int item = tid + i * kAttnThreads;
+      if (item < VCH) {
+        const int kp = item / CPR, c = item % CPR;
+        const int k0 = min(kv0 + 2 * kp, Tk - 1), k1 = min(kv0 + 2 * kp + 1, Tk - 1);
+        rv[i][0] = *reinterpret_cast<const u32x4_t*>(Vb + k0 * v_st + c * EPC);
+        rv[i][1] = *reinterpret_cast<const u32x4_t*>(Vb + k1 * v_st + c * EPC);
+      }
+    }
+  };
+  auto swrite = [&](int buf) {
+    uint8_t* sk = smem + buf * STAGE;
+    uint8_t* sv = sk + KBYTES;
+#pragma unroll
+    for (int i = 0; i < KL; ++i) {
+      const int item = tid + i * kAttnThreads;
+      if (item < KCH) {
+        const int key = item / CPR, c = item % CPR;
+        *reinterpret_cast<u32x4_t*>(sk + key * KROW + ((c ^ (key & SWZ)) << 4)) = rk[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VL; ++i) {
+      const int item = tid + i * kAttnThreads;
+      if (item < VCH) {
+        const int kp = item / CPR, c = item % CPR;
+        if constexpr (sizeof(T) == 2) {
+          // 8 head_dim values of two consecutive keys -> 8 words [d][2kp, 2kp+1].
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t a = rv[i][0][e], bb = rv[i][1][e];
+            const int d = c * EPC + 2 * e;
+            *reinterpret_cast<uint32_t*>(sv + d * VROW + kp * 4) = (a & 0xffffu) | (bb << 16);
+            *reinterpret_cast<uint32_t*>(sv + (d + 1) * VROW + kp * 4) = (a >> 16) | (bb & 0xffff0000u);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int d = c * EPC + e;
+            *reinterpret_cast<u32x2_t*>(sv + d * VROW + kp * 8) = u32x2_t{rv[i][0][e], rv[i][1][e]};
+          }
+        }
+      }
+    }
+  };
+
+  f32x4_t o_acc[QT][ND];
+  float m_run[QT], l_run[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    m_run[qt] = -INFINITY;
+    l_run[qt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) o_acc[qt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  if (n_kv > 0) {
+    gload(0);
+    swrite(0);
+  }
+  __syncthreads();
+  for (int j = 0; j < n_kv; ++j) {
+    const int buf = j & 1;
+    const int kv0 = j * BKV;
+    if (j + 1 < n_kv) gload(j + 1);
+    const uint8_t* sk = smem + buf * STAGE;
+    const uint8_t* sv = sk + KBYTES;
+    // A wave whose queries all precede this key block has nothing to do here.
+    if (wave_live && !(causal && kv0 > wave_last)) {
+      f32x4_t s[QT][4];
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) s[qt][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        const int c = 4 * ks + g;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+          const int key = kt * 16 + frow;
+          const u32x4_t kf = (c < CPR) ? *reinterpret_cast<const u32x4_t*>(
+                                             sk + key * KROW + ((c ^ (key & SWZ)) << 4))
+                                       : u32x4_t{0, 0, 0, 0};
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) AttnMfma<T>::run(kf, qf[qt][ks], s[qt][kt]);
+        }
+      }
+      // Online softmax (base 2).  Masking only where the block can be partial.
+      const bool need_mask = (causal && kv0 + BKV - 1 > wave_q0 + off) || (kv0 + BKV > Tk);
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        const int qpos = wave_q0 + qt * 16 + frow + off;
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float x = s[qt][kt][r] * scale_log2;
+            if (need_mask) {
+              const int key = kv0 + kt * 16 + 4 * g + r;
+              if (key >= Tk || (causal && key > qpos)) x = -INFINITY;
+            }
+            s[qt][kt][r] = x;
+            mloc = fmaxf(mloc, x);
+          }
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        const float m_new = fmaxf(m_run[qt], mloc);
+        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run[qt] - m_use);
+        m_run[qt] = m_new;
+        float lsum = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float p = __builtin_amdgcn_exp2f(s[qt][kt][r] - m_use);
+            s[qt][kt][r] = p;
+            lsum += p;
+          }
+        l_run[qt] = l_run[qt] * alpha + lsum;
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o_acc[qt][dt][r] *= alpha;
+      }
+      // O^T += V^T P^T
+      if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          u32x4_t pf[QT];
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt)
+            pf[qt] = u32x4_t{pack_bf16x2(s[qt][2 * c][0], s[qt][2 * c][1]),
+                             pack_bf16x2(s[qt][2 * c][2], s[qt][2 * c][3]),
+                             pack_bf16x2(s[qt][2 * c + 1][0], s[qt][2 * c + 1][1]),
+                             pack_bf16x2(s[qt][2 * c + 1][2], s[qt][2 * c + 1][3])};
+#pragma unroll
+          for (int dt = 0; dt < ND; ++dt) {
+            const uint8_t* row = sv + (dt * 16 + frow) * VROW;
+            const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(row + (32 * c + 4 * g) * 2);
+            const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(row + (32 * c + 16 + 4 * g) * 2);
+            const u32x4_t vf = {lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) AttnMfma<T>::run(vf, pf[qt], o_acc[qt][dt]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          u32x4_t pf[QT];
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt)
+            pf[qt] = u32x4_t{__float_as_uint(s[qt][c][0]), __float_as_uint(s[qt][c][1]),
+                             __float_as_uint(s[qt][c][2]), __float_as_uint(s[qt][c][3])};
+#pragma unroll
+          for (int dt = 0; dt < ND; ++dt) {
+            const uint8_t* row = sv + (dt * 16 + frow) * VROW;
+            const u32x4_t vf = *reinterpret_cast<const u32x4_t*>(row + (16 * c + 4 * g) * 4);
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) AttnMfma<T>::run(vf, pf[qt], o_acc[qt][dt]);
+          }
+        }
+      }
+    }
+    if (j + 1 < n_kv) swrite(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Normalise and store: lane holds O[query][dt*16 + 4g .. +3].
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int qi = wave_q0 + qt * 16 + frow;
+    float l = l_run[qt];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    if (qi >= Tq) continue;
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    T* orow = O + b * o_sb + h * o_sh + qi * o_st;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) {
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = o_acc[qt][dt][r] * inv;
+      store4_o(orow + dt * 16 + 4 * g, v);
+    }
+  }
+}
+
+template <typename T, int HD>
+static int launch_attn(const void* q, const void* k, const void* v, void* o, int B, int H, int Tq,
+                       int Tk, const int64_t* st, float scale, int causal, hipStream_t s) {
+  const int n_bh = B * H;
+  const int n_qblk = (Tq + kAttnBQ - 1) / kAttnBQ;
+  const int64_t blocks = static_cast<int64_t>(n_bh) * n_qblk;
+  if (blocks > 0x7fffffff) return CGPT_ESHAPE;
+  const float scale_log2 = scale * 1.4426950408889634f;
+  hipLaunchKernelGGL((attn_fwd_kernel<T, HD>), dim3(static_cast<unsigned>(blocks)),
+                     dim3(kAttnThreads), 0, s, static_cast<const T*>(q), static_cast<const T*>(k),
+                     static_cast<const T*>(v), static_cast<T*>(o), H, Tq, Tk, st[0], st[1], st[2],
+                     st[3], st[4], st[5], st[6], st[7], st[8], st[9], st[10], st[11], scale_log2,
+                     causal, n_bh);
+  return hip_status(hipGetLastError());
+}
+
+template <typename T>
+static int dispatch_hd(int hd, const void* q, const void* k, const void* v, void* o, int B, int H,
+                       int Tq, int Tk, const int64_t* st, float scale, int causal, hipStream_t s) {
+  switch (hd) {
+    case 16: return launch_attn<T, 16>(q, k, v, o, B, H, Tq, Tk, st, scale, causal, s);
+    case 32: return launch_attn<T, 32>(q, k, v, o, B, H, Tq, Tk, st, scale, causal, s);
+    case 64: return launch_attn<T, 64>(q, k, v, o, B, H, Tq, Tk, st, scale, causal, s);
+    case 128: return launch_attn<T, 128>(q, k, v, o, B, H, Tq, Tk, st, scale, causal, s);
+    default: return CGPT_ESHAPE;
+  }
+}
+
+}  // namespace cgpt
+
+extern "C" int cgpt_attention_fwd(const void* q, const void* k, const void* v, void* o, int64_t B,
+                                  int64_t H, int64_t Tq, int64_t Tk, int64_t head_dim,
+                                  int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t k_sb,
+                                  int64_t k_sh, int64_t k_st, int64_t v_sb, int64_t v_sh,
+                                  int64_t v_st, int64_t o_sb, int64_t o_sh, int64_t o_st,
+                                  float scale, int causal, int dtype, void* stream) {
+  using namespace cgpt;
+  if (B < 0 || H < 0 || Tq < 0 || Tk < 0) return CGPT_EINVAL;
+  if (B == 0 || H == 0 || Tq == 0) return CGPT_OK;
+  if (q == nullptr || k == nullptr || v == nullptr || o == nullptr) return CGPT_EINVAL;
+  if (Tk < Tq || Tk == 0) return CGPT_EINVAL;
+  if (B * H > 0x7fffffff || Tk > 0x7fffffff) return CGPT_ESHAPE;
+  if (dtype != CGPT_F32 && dtype != CGPT_BF16) return CGPT_EDTYPE;
+  const int64_t epc = dtype == CGPT_F32 ? 4 : 8;
+  const int64_t st[12] = {q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, o_sb, o_sh, o_st};
+  // 16-byte vector loads of Q/K/V rows and 4-element stores of O need every
+  // row start to stay 16-byte (8-byte for O in bf16) aligned.
+  for (int i = 0; i < 9; ++i)
+    if (st[i] < 0 || st[i] % epc != 0) return CGPT_EINVAL;
+  for (int i = 9; i < 12; ++i)
+    if (st[i] < 0 || st[i] % 4 != 0) return CGPT_EINVAL;
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+       reinterpret_cast<uintptr_t>(v)) & 15)
+    return CGPT_EINVAL;
+  if (reinterpret_cast<uintptr_t>(o) & (dtype == CGPT_F32 ? 15 : 7)) return CGPT_EINVAL;
+  if (!(scale > 0.f)) return CGPT_EINVAL;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int b = static_cast<int>(B), h = static_cast<int>(H);
+  const int tq = static_cast<int>(Tq), tk = static_cast<int>(Tk);
+  const int hd = static_cast<int>(head_dim);
+  if (dtype == CGPT_BF16) return dispatch_hd<bf16_t>(hd, q, k, v, o, b, h, tq, tk, st, scale, causal != 0, s);
+  return dispatch_hd<float>(hd, q, k, v, o, b, h, tq, tk, st, scale, causal != 0, s);
+}

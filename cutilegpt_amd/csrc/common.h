@@ -1,0 +1,104 @@
+// Shared device helpers for the gfx950 (CDNA4) kernels of cutilegpt_amd.
+//
+// Conventions used by every kernel in this directory:
+//  * one wavefront = 64 lanes; blocks are multiples of 64 threads;
+//  * bf16 is stored as raw uint16_t bit patterns and converted with
+//    round-to-nearest-even; arithmetic is always fp32;
+//  * 16-byte vector accesses (dwordx4) for every streaming load/store.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/cgpt.h"
+
+namespace cgpt {
+
+typedef uint16_t bf16_t;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float bf16_to_f32(bf16_t v) {
+  return __uint_as_float(static_cast<uint32_t>(v) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16; NaN stays a (quiet) NaN.
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<bf16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<bf16_t>(u >> 16);
+}
+
+// Two fp32 -> packed pair of bf16 (low half = a).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+}
+
+// Element type traits: load/store a float from/to T storage.
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static constexpr int kVec = 4;  // elements per 16-byte vector
+  __device__ static float load(const float* p) { return *p; }
+  __device__ static void store(float* p, float v) { *p = v; }
+};
+template <> struct Elem<bf16_t> {
+  static constexpr int kVec = 8;
+  __device__ static float load(const bf16_t* p) { return bf16_to_f32(*p); }
+  __device__ static void store(bf16_t* p, float v) { *p = f32_to_bf16(v); }
+};
+
+// Load/store 16 bytes as kVec floats.
+__device__ __forceinline__ void load_vec(const float* p, float* out) {
+  f32x4_t v = *reinterpret_cast<const f32x4_t*>(p);
+  out[0] = v[0]; out[1] = v[1]; out[2] = v[2]; out[3] = v[3];
+}
+__device__ __forceinline__ void load_vec(const bf16_t* p, float* out) {
+  u32x4_t v = *reinterpret_cast<const u32x4_t*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(v[i] << 16);
+    out[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ void store_vec(float* p, const float* in) {
+  f32x4_t v = {in[0], in[1], in[2], in[3]};
+  *reinterpret_cast<f32x4_t*>(p) = v;
+}
+__device__ __forceinline__ void store_vec(bf16_t* p, const float* in) {
+  u32x4_t v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = pack_bf16x2(in[2 * i], in[2 * i + 1]);
+  *reinterpret_cast<u32x4_t*>(p) = v;
+}
+
+// Butterfly sum / max across the 64 lanes of a wavefront.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// tanh-approximate GELU written through the identity
+//   0.5 x (1 + tanh(u)) = x / (1 + exp(-2u)),  u = sqrt(2/pi) (x + 0.044715 x^3),
+// with exp(-2u) = 2^(-2u log2 e) on the hardware exp2.  Saturates cleanly:
+// u -> +inf gives x, u -> -inf gives -0.
+__device__ __forceinline__ float gelu_tanh(float x) {
+  constexpr float kSqrt2OverPi = 0.7978845608028654f;
+  constexpr float kCoef = 0.044715f;
+  constexpr float kNeg2Log2e = -2.8853900817779268f;  // -2 / ln 2
+  float u = kSqrt2OverPi * (x + kCoef * x * x * x);
+  float e = __builtin_amdgcn_exp2f(kNeg2Log2e * u);
+  return x / (1.0f + e);
+}
+
+// Error codes shared with the C ABI (see include/cgpt.h).
+__host__ __forceinline__ int hip_status(hipError_t e) {
+  return e == hipSuccess ? CGPT_OK : static_cast<int>(e);
+}
+
+}  // namespace cgpt

@@ -1,0 +1,104 @@
+// Token + position embedding gather (HBM-bound, one wavefront per token).
+//
+// out[i, :] = wte[idx[i], :] (+ wpe[pos0 + i % T, :]); lane l of the wave moves
+// columns [4(64c + l), 4(64c + l) + 4) for each 256-column chunk c, so each row
+// is read and written with contiguous, fully coalesced spans.  Out-of-range
+// ids/positions are clamped (no out-of-bounds read is possible) and reported
+// through an optional device flag.
+#include "common.h"
+
+namespace cgpt {
+
+constexpr int kEmbThreads = 256;
+constexpr int kEmbTokensPerBlock = kEmbThreads / 64;
+
+__device__ __forceinline__ void ld4(const float* p, float* v) { load_vec(p, v); }
+__device__ __forceinline__ void ld4(const bf16_t* p, float* v) {
+  u32x2_t u = *reinterpret_cast<const u32x2_t*>(p);
+  v[0] = __uint_as_float(u[0] << 16);
+  v[1] = __uint_as_float(u[0] & 0xffff0000u);
+  v[2] = __uint_as_float(u[1] << 16);
+  v[3] = __uint_as_float(u[1] & 0xffff0000u);
+}
+__device__ __forceinline__ void st4(float* p, const float* v) { store_vec(p, v); }
+__device__ __forceinline__ void st4(bf16_t* p, const float* v) {
+  u32x2_t u = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  *reinterpret_cast<u32x2_t*>(p) = u;
+}
+
+template <typename TW, typename TO>
+__global__ __launch_bounds__(kEmbThreads) void embedding_kernel(
+    const int64_t* __restrict__ idx, const TW* __restrict__ wte, const TW* __restrict__ wpe,
+    TO* __restrict__ out, int64_t n_tokens, int64_t T, int D, int64_t vocab, int64_t pos0,
+    int64_t n_pos, int* err_flag) {
+  const int lane = threadIdx.x & 63;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kEmbTokensPerBlock + (threadIdx.x >> 6);
+  if (i >= n_tokens) return;
+  int64_t id = idx[i];
+  bool bad = false;
+  if (id < 0 || id >= vocab) {
+    bad = true;
+    id = id < 0 ? 0 : vocab - 1;
+  }
+  int64_t pos = pos0 + i % T;
+  if (wpe != nullptr && (pos < 0 || pos >= n_pos)) {
+    bad = true;
+    pos = pos < 0 ? 0 : n_pos - 1;
+  }
+  if (bad && err_flag != nullptr && lane == 0) *err_flag = 1;
+  const TW* trow = wte + id * D;
+  const TW* prow = wpe != nullptr ? wpe + pos * D : nullptr;
+  TO* orow = out + i * D;
+  for (int col = lane * 4; col < D; col += 256) {
+    float v[4];
+    ld4(trow + col, v);
+    if (prow != nullptr) {
+      float p[4];
+      ld4(prow + col, p);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] += p[j];
+    }
+    st4(orow + col, v);
+  }
+}
+
+template <typename TW, typename TO>
+static int launch_emb(const int64_t* idx, const void* wte, const void* wpe, void* out,
+                      int64_t n_tokens, int64_t T, int D, int64_t vocab, int64_t pos0,
+                      int64_t n_pos, int* err, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((n_tokens + kEmbTokensPerBlock - 1) / kEmbTokensPerBlock));
+  hipLaunchKernelGGL((embedding_kernel<TW, TO>), grid, dim3(kEmbThreads), 0, s, idx,
+                     static_cast<const TW*>(wte), static_cast<const TW*>(wpe),
+                     static_cast<TO*>(out), n_tokens, T, D, vocab, pos0, n_pos, err);
+  return hip_status(hipGetLastError());
+}
+
+}  // namespace cgpt
+
+extern "C" int cgpt_embedding(const int64_t* idx, const void* wte, const void* wpe, void* out,
+                              int64_t n_tokens, int64_t T, int64_t D, int64_t vocab,
+                              int64_t pos0, int64_t n_pos, int w_dtype, int out_dtype,
+                              int* err_flag, void* stream) {
+  using namespace cgpt;
+  if (n_tokens < 0 || D <= 0 || vocab <= 0) return CGPT_EINVAL;
+  if (n_tokens == 0) return CGPT_OK;
+  if (idx == nullptr || wte == nullptr || out == nullptr || T <= 0) return CGPT_EINVAL;
+  if (wpe != nullptr && n_pos <= 0) return CGPT_EINVAL;
+  if (D % 4 != 0 || D > (1 << 20)) return CGPT_ESHAPE;
+  const uintptr_t wa = (w_dtype == CGPT_F32) ? 15 : 7;
+  const uintptr_t oa = (out_dtype == CGPT_F32) ? 15 : 7;
+  if ((reinterpret_cast<uintptr_t>(wte) & wa) || (reinterpret_cast<uintptr_t>(wpe) & wa) ||
+      (reinterpret_cast<uintptr_t>(out) & oa) || (reinterpret_cast<uintptr_t>(idx) & 7))
+    return CGPT_EINVAL;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int d = static_cast<int>(D);
+  if (w_dtype == CGPT_F32 && out_dtype == CGPT_F32)
+    return launch_emb<float, float>(idx, wte, wpe, out, n_tokens, T, d, vocab, pos0, n_pos, err_flag, s);
+  if (w_dtype == CGPT_BF16 && out_dtype == CGPT_F32)
+    return launch_emb<bf16_t, float>(idx, wte, wpe, out, n_tokens, T, d, vocab, pos0, n_pos, err_flag, s);
+  if (w_dtype == CGPT_BF16 && out_dtype == CGPT_BF16)
+    return launch_emb<bf16_t, bf16_t>(idx, wte, wpe, out, n_tokens, T, d, vocab, pos0, n_pos, err_flag, s);
+  if (w_dtype == CGPT_F32 && out_dtype == CGPT_BF16)
+    return launch_emb<float, bf16_t>(idx, wte, wpe, out, n_tokens, T, d, vocab, pos0, n_pos, err_flag, s);
+  return CGPT_EDTYPE;
+}

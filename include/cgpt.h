@@ -1,0 +1,139 @@
+/*
+ * cgpt.h — C ABI of libcgpt.so, the gfx950 (MI355X / CDNA4) kernels behind
+ * cutilegpt_amd's drop-in replacements for cutileGPT's kernel functions.
+ *
+ * Every entry point:
+ *   - takes plain device pointers, element counts and element strides (no
+ *     framework types), and a HIP stream passed as `void*` (hipStream_t);
+ *   - launches asynchronously on that stream and never allocates or frees;
+ *   - validates its arguments before launching and returns a status:
+ *       0            CGPT_OK
+ *       < 0          an argument error (CGPT_E*), nothing was launched
+ *       > 0          a hipError_t from the launch
+ *   - has no mutable global state, so concurrent calls on different streams
+ *     are safe.
+ *
+ * Element types are CGPT_F32 (IEEE fp32) and CGPT_BF16 (bfloat16 bit
+ * patterns); all arithmetic is fp32, bf16 outputs are rounded to nearest even.
+ *
+ * Reference citations are relative to the falcons-eyes/cutileGPT checkout.
+ */
+#ifndef CGPT_H_
+#define CGPT_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CGPT_ABI_VERSION 1
+
+/* status codes */
+#define CGPT_OK 0
+#define CGPT_EINVAL (-1)       /* bad pointer, size, stride or alignment */
+#define CGPT_EDTYPE (-2)       /* unsupported dtype combination */
+#define CGPT_ESHAPE (-3)       /* shape outside what the kernels support */
+
+/* element types */
+#define CGPT_F32 0
+#define CGPT_BF16 1
+
+/* GEMM epilogues */
+#define CGPT_EPI_NONE 0        /* C = A W^T                                  */
+#define CGPT_EPI_BIAS 1        /* C = A W^T + bias                           */
+#define CGPT_EPI_BIAS_GELU 2   /* C = gelu_tanh(A W^T + bias)                */
+
+/* ABI version (CGPT_ABI_VERSION) of the loaded library. */
+int cgpt_version(void);
+
+/* Human-readable text for a status returned by any entry point. */
+const char* cgpt_status_string(int status);
+
+/*
+ * Element-wise tanh-approximate GELU, y = 0.5 x (1 + tanh(sqrt(2/pi)(x + 0.044715 x^3))).
+ * x and y hold n elements of `dtype`, contiguous; y may alias x.
+ * Replaces cutile_gelu, cutile_gpt/kernels/gelu.py:71-110 (kernel :20-41).
+ */
+int cgpt_gelu(const void* x, void* y, int64_t n, int dtype, void* stream);
+
+/*
+ * Fused residual add + LayerNorm over rows of `cols` contiguous elements:
+ *   s     = x + delta              (delta may be NULL: s = x)
+ *   x_out = s                      (x_out may be NULL, or alias x)
+ *   y     = (s - mean(s)) / sqrt(var(s) + eps) * gamma + beta   (biased var)
+ * Row r of x / delta / x_out / y starts at r * cols.  gamma and beta hold
+ * `cols` elements of `param_dtype`.  Statistics are accumulated in fp32.
+ * Replaces cutile_layer_norm, cutile_gpt/kernels/layernorm.py:77-135 (kernel
+ * :24-74), fused with the residual adds at cutile_gpt/models/gpt.py:155,174.
+ */
+int cgpt_add_layernorm(const void* x, const void* delta, void* x_out,
+                       const void* gamma, const void* beta, void* y,
+                       int64_t rows, int64_t cols, float eps,
+                       int x_dtype, int delta_dtype, int param_dtype, int y_dtype,
+                       void* stream);
+
+/*
+ * C[M,N] = epilogue(A[M,K] * W[N,K]^T (+ bias[N])).
+ * A row-major with leading dimension lda, W row-major (out_features, in_features)
+ * with leading dimension ldw — the nn.Linear / cutileGPT `weight` layout, so no
+ * transposed copy is needed — C row-major with leading dimension ldc.
+ * in_dtype is the type of A and W (both CGPT_BF16 -> bf16 MFMA, both CGPT_F32 ->
+ * fp32 MFMA); accumulation is fp32; bias (bias_dtype) is added in fp32; C is
+ * written as out_dtype.  Requires K % 8 == 0 (bf16) or K % 4 == 0 (fp32), lda /
+ * ldw multiples of 8 (bf16) or 4 (fp32) elements and 16-byte aligned A and W.
+ * `tile` selects a tile configuration (CGPT_TILE_AUTO = library heuristic).
+ * Replaces cutile_linear / cutile_linear_bias, cutile_gpt/kernels/linear.py:112-222
+ * (kernels :37-109); CGPT_EPI_BIAS_GELU also absorbs cutile_gelu at
+ * cutile_gpt/models/gpt.py:167.
+ */
+#define CGPT_TILE_AUTO (-1)
+int cgpt_gemm(const void* a, const void* w, const void* bias, void* c,
+              int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldc,
+              int in_dtype, int bias_dtype, int out_dtype, int epilogue, int tile,
+              void* stream);
+
+/* Number of GEMM tile configurations compiled into the library. */
+int cgpt_gemm_num_tiles(void);
+
+/*
+ * Causal (or full) softmax attention, O = softmax(Q K^T * scale + mask) V,
+ * for B batches x H heads; Q has Tq rows, K/V have Tk rows (Tk >= Tq); query i
+ * sits at absolute position Tk - Tq + i and, when `causal`, sees keys j <= that
+ * position.  Every tensor is addressed as base + b*sb + h*sh + t*st + d with
+ * unit stride along head_dim, so Q/K/V may be strided views into one fused QKV
+ * projection buffer (B, T, 3, H, hd) and O may be written straight into
+ * (B, T, H, hd).  Softmax statistics are fp32; P is rounded to `dtype` before
+ * the P*V product.  head_dim in {16, 32, 64, 128}.
+ * Replaces cutile_causal_attention, cutile_gpt/kernels/attention.py:119-175
+ * (kernel :24-116) and the QKV split/transpose copies at
+ * cutile_gpt/models/gpt.py:133-146.
+ */
+int cgpt_attention_fwd(const void* q, const void* k, const void* v, void* o,
+                       int64_t B, int64_t H, int64_t Tq, int64_t Tk, int64_t head_dim,
+                       int64_t q_sb, int64_t q_sh, int64_t q_st,
+                       int64_t k_sb, int64_t k_sh, int64_t k_st,
+                       int64_t v_sb, int64_t v_sh, int64_t v_st,
+                       int64_t o_sb, int64_t o_sh, int64_t o_st,
+                       float scale, int causal, int dtype, void* stream);
+
+/*
+ * Token (+ position) embedding gather:
+ *   out[i, :] = wte[idx[i], :] (+ wpe[pos0 + i % T, :])
+ * for i < n_tokens; idx holds int64 token ids; wpe may be NULL (plain gather).
+ * Ids outside [0, vocab) or positions outside [0, n_pos) are clamped into range
+ * (so the kernel never reads out of bounds) and, when err_flag is not NULL,
+ * set *err_flag (a device int) to 1.
+ * Replaces cutile_embedding, cutile_gpt/kernels/embedding.py:54-109 (kernel
+ * :23-51), fused with the token+position add at cutile_gpt/models/gpt.py:110-113.
+ */
+int cgpt_embedding(const int64_t* idx, const void* wte, const void* wpe, void* out,
+                   int64_t n_tokens, int64_t T, int64_t D, int64_t vocab,
+                   int64_t pos0, int64_t n_pos, int w_dtype, int out_dtype,
+                   int* err_flag, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CGPT_H_ */

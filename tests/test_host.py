@@ -1,0 +1,132 @@
+"""Host-side logic on the CPU: the C ABI library, argument validation, config
+presets and the HF checkpoint loader.  No kernel is launched here."""
+
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "cgpt.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(cgpt_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_header_symbol():
+    from cutilegpt_amd import _lib
+    lib = _lib.load()
+    names = header_functions()
+    assert len(names) >= 8
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    assert lib.cgpt_version() == _lib.ABI_VERSION
+
+
+def test_status_strings():
+    from cutilegpt_amd import _lib
+    lib = _lib.load()
+    assert lib.cgpt_status_string(0) == b"ok"
+    assert b"invalid" in lib.cgpt_status_string(-1)
+    assert b"dtype" in lib.cgpt_status_string(-2)
+    assert b"shape" in lib.cgpt_status_string(-3)
+
+
+def test_abi_rejects_bad_arguments_before_launch():
+    """Argument errors return negative status without touching the GPU (the
+    pointers here are never dereferenced)."""
+    from cutilegpt_amd import _lib
+    lib = _lib.load()
+    fake = 1 << 20  # 16-byte aligned, never dereferenced
+    # gemm: K not a multiple of 8 for bf16, bad epilogue, missing bias, misaligned A, bad dtype
+    assert lib.cgpt_gemm(fake, fake, None, fake, 4, 4, 12, 12, 12, 4, 1, 1, 1, 0, -1, None) == -3
+    assert lib.cgpt_gemm(fake, fake, None, fake, 4, 4, 16, 16, 16, 4, 1, 1, 1, 7, -1, None) == -1
+    assert lib.cgpt_gemm(fake, fake, None, fake, 4, 4, 16, 16, 16, 4, 1, 1, 1, 1, -1, None) == -1
+    assert lib.cgpt_gemm(fake + 2, fake, None, fake, 4, 4, 16, 16, 16, 4, 1, 1, 1, 0, -1, None) == -1
+    assert lib.cgpt_gemm(fake, fake, None, fake, 4, 4, 16, 16, 16, 4, 5, 1, 1, 0, -1, None) == -2
+    assert lib.cgpt_gemm(fake, fake, None, fake, 4, 4, 16, 8, 16, 4, 1, 1, 1, 0, -1, None) == -1
+    assert lib.cgpt_gemm(fake, fake, None, fake, 4, 4, 16, 16, 16, 4, 1, 1, 1, 0, 99, None) == -1
+    # empty problems are a no-op success
+    assert lib.cgpt_gemm(None, None, None, None, 0, 4, 16, 16, 16, 4, 1, 1, 1, 0, -1, None) == 0
+    # layernorm: cols not multiple of 4 / too wide / bad dtype / null gamma
+    assert lib.cgpt_add_layernorm(fake, None, None, fake, fake, fake, 2, 6, 1e-5, 0, 0, 0, 0, None) == -3
+    assert lib.cgpt_add_layernorm(fake, None, None, fake, fake, fake, 2, 8192, 1e-5, 0, 0, 0, 0, None) == -3
+    assert lib.cgpt_add_layernorm(fake, None, None, fake, fake, fake, 2, 8, 1e-5, 3, 0, 0, 0, None) == -2
+    assert lib.cgpt_add_layernorm(fake, None, None, None, fake, fake, 2, 8, 1e-5, 0, 0, 0, 0, None) == -1
+    # attention: unsupported head_dim, Tk < Tq, unaligned strides, bad scale
+    args = lambda hd, tq, tk, st, scale: (fake, fake, fake, fake, 1, 1, tq, tk, hd,
+                                          *([0, 0, st] * 4), scale, 1, 1, None)
+    assert lib.cgpt_attention_fwd(*args(48, 4, 4, 48, 0.1)) == -3
+    assert lib.cgpt_attention_fwd(*args(64, 8, 4, 64, 0.1)) == -1
+    assert lib.cgpt_attention_fwd(*args(64, 4, 4, 60, 0.1)) == -1
+    assert lib.cgpt_attention_fwd(*args(64, 4, 4, 64, 0.0)) == -1
+    # gelu / embedding
+    assert lib.cgpt_gelu(fake, fake, 10, 9, None) == -2
+    assert lib.cgpt_gelu(None, None, 0, 0, None) == 0
+    assert lib.cgpt_embedding(fake, fake, None, fake, 4, 4, 6, 10, 0, 0, 0, 0, None, None) == -3
+
+
+def test_wrappers_reject_host_tensors():
+    import cutilegpt_amd as cg
+    x = torch.randn(4, 8)
+    with pytest.raises(ValueError):
+        cg.cutile_gelu(x)
+    with pytest.raises(ValueError):
+        cg.cutile_layer_norm(x, torch.ones(8), torch.zeros(8))
+    with pytest.raises(ValueError):
+        cg.cutile_linear(x, torch.randn(3, 8))
+    with pytest.raises(ValueError):
+        cg.cutile_causal_attention(x.view(1, 1, 4, 8), x.view(1, 1, 4, 8), x.view(1, 1, 4, 8), 1)
+    with pytest.raises(ValueError):
+        cg.cutile_embedding(torch.tensor([1, 2]), x)
+
+
+def test_config_presets_match_reference():
+    from cutilegpt_amd import GPTConfig
+    # cutile_gpt/models/config.py:19-87
+    expect = {"nano": (3, 3, 48, 128), "micro": (4, 4, 128, 256), "mini": (6, 6, 192, 256),
+              "gpt2": (12, 12, 768, 1024), "gpt2-medium": (24, 16, 1024, 1024),
+              "gpt2-large": (36, 20, 1280, 1024), "gpt2-xl": (48, 25, 1600, 1024),
+              "tile-small": (4, 4, 64, 128), "tile-medium": (6, 4, 128, 256),
+              "tile-large": (8, 8, 256, 512)}
+    for name, (l, h, d, bs) in expect.items():
+        c = GPTConfig.from_name(name)
+        assert (c.n_layer, c.n_head, c.n_embd, c.block_size, c.vocab_size) == (l, h, d, bs, 50257)
+    with pytest.raises(ValueError):
+        GPTConfig.from_name("gpt5")
+
+
+def test_hf_checkpoint_roundtrip_and_transformers_agree(tmp_path):
+    """save_hf_checkpoint writes a directory that transformers itself loads,
+    and load_hf_checkpoint maps it back to the internal layout exactly."""
+    from cutilegpt_amd.config import GPTConfig
+    from cutilegpt_amd.hf_loader import load_hf_checkpoint, save_hf_checkpoint
+    from oracle import gpt_ref as R
+    from transformers import GPT2LMHeadModel
+
+    cfg = GPTConfig(n_layer=2, n_head=2, n_embd=32, block_size=64, vocab_size=50257)
+    w = R.init_weights(2, 2, 32, block_size=64, seed=11)
+    save_hf_checkpoint(str(tmp_path), w, cfg)
+    w2, cfg2 = load_hf_checkpoint(str(tmp_path))
+    assert cfg2 == cfg
+    for k in w:
+        assert torch.equal(w[k], w2[k]), k
+    assert w2["lm_head.weight"] is w2["wte"]
+    m = GPT2LMHeadModel.from_pretrained(str(tmp_path)).eval()
+    ids = torch.randint(0, 50257, (1, 20), generator=torch.Generator().manual_seed(0))
+    with torch.no_grad():
+        ref = m(ids).logits
+    out = R.gpt_forward(w2, ids, 2, R.FLOWS["fp32"])
+    assert (out - ref).abs().max().item() < 1e-5
+
+
+def test_tile_table_lookup():
+    from cutilegpt_amd import tiles, _lib
+    assert tiles.gemm_tile(_lib.CGPT_BF16, 3, 5, 8) == _lib.TILE_AUTO
+    n = _lib.load().cgpt_gemm_num_tiles()
+    for key, t in tiles.TABLE.items():
+        assert 0 <= t < n, key

@@ -1,0 +1,245 @@
+"""Kernel parity on the GPU: every HIP kernel against the CPU oracle (fp64)
+at small and ragged shapes, and at the standalone-kernel benchmark sizes.
+
+Tolerances: fp32 outputs within a few fp32 ulps of the exact result scaled
+by the problem (stated per test); bf16 outputs within one bf16 rounding
+(relative 2^-8) plus the fp32 accumulation error.
+"""
+
+import math
+
+import pytest
+import torch
+
+import cutilegpt_amd as cg
+from cutilegpt_amd import _lib
+from oracle import gpt_ref as R
+
+pytestmark = pytest.mark.gpu
+
+F32, BF16 = torch.float32, torch.bfloat16
+
+
+def randn(*shape, seed=0, dtype=F32, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(dtype)
+
+
+def close(out, ref, atol, rtol, what=""):
+    out = out.detach().cpu().double()
+    ref = ref.detach().cpu().double()
+    err = (out - ref).abs()
+    bound = atol + rtol * ref.abs()
+    bad = err > bound
+    assert not bad.any(), (f"{what}: {int(bad.sum())} of {bad.numel()} outside tolerance, "
+                           f"max err {err.max().item():.3e}")
+
+
+# --------------------------------------------------------------------- GELU
+
+@pytest.mark.parametrize("dtype", [F32, BF16])
+@pytest.mark.parametrize("n", [1, 7, 4099, 32 * 512 * 768])
+def test_gelu(gpu, dtype, n):
+    x = randn(n, seed=n, dtype=dtype)
+    y = cg.cutile_gelu(x.to(gpu))
+    ref = R.gelu_tanh(x.double())
+    if dtype == F32:
+        close(y, ref, 2e-6, 2e-6, "gelu fp32")
+    else:
+        close(y, ref, 1e-6, 2 ** -8, "gelu bf16")
+
+
+def test_gelu_3d_shape_and_special_values(gpu):
+    x = torch.tensor([0.0, -0.0, 30.0, -30.0, 1e-8, -1e-8, 5.0, -5.0], dtype=F32)
+    y = cg.cutile_gelu(x.view(2, 2, 2).to(gpu))
+    assert y.shape == (2, 2, 2)
+    close(y.view(-1), R.gelu_tanh(x.double()), 1e-7, 1e-6, "gelu special")
+
+
+# ---------------------------------------------------------------- LayerNorm
+
+@pytest.mark.parametrize("rows,cols", [(1, 4), (5, 48), (37, 768), (3, 1600), (7, 4096),
+                                       (16384, 768)])
+@pytest.mark.parametrize("xd,yd", [(F32, F32), (BF16, BF16), (F32, BF16)])
+def test_layer_norm(gpu, rows, cols, xd, yd):
+    x = randn(rows, cols, seed=rows + cols, dtype=xd, scale=2.0) + 0.5
+    w = (1 + randn(cols, seed=1, scale=0.1)).to(xd)
+    b = randn(cols, seed=2, scale=0.1).to(xd)
+    y = cg.add_layer_norm(x.to(gpu), None, w.to(gpu), b.to(gpu), out_dtype=yd)
+    ref = R.layer_norm(x.double(), w.double(), b.double())
+    if yd == F32:
+        close(y, ref, 1e-5, 1e-5, "ln fp32")
+    else:
+        close(y, ref, 1e-5, 2 ** -8 + 1e-5, "ln bf16")
+
+
+@pytest.mark.parametrize("dd", [F32, BF16])
+def test_add_layer_norm_writes_residual(gpu, dd):
+    rows, cols = 300, 768
+    x = randn(rows, cols, seed=3)
+    d = randn(rows, cols, seed=4, dtype=dd)
+    w, b = randn(cols, seed=5) + 1, randn(cols, seed=6)
+    xg = x.to(gpu)
+    y = cg.add_layer_norm(xg, d.to(gpu), w.to(gpu), b.to(gpu), out_dtype=BF16, x_out=xg)
+    s = x.double() + d.double()
+    close(xg, s, 1e-6, 1e-6, "residual")  # x_out == x + delta (in place)
+    close(y, R.layer_norm(s, w.double(), b.double()), 1e-5, 2 ** -8 + 1e-5, "add+ln")
+
+
+def test_layer_norm_constant_rows(gpu):
+    x = torch.full((4, 768), 3.5)
+    beta = randn(768, seed=7)
+    y = cg.cutile_layer_norm(x.to(gpu), torch.ones(768, device=gpu), beta.to(gpu))
+    close(y, beta.expand(4, 768), 1e-6, 0, "constant row -> beta")
+
+
+# --------------------------------------------------------------------- GEMM
+
+GEMM_SHAPES = [(1, 1, 8), (17, 33, 40), (64, 64, 64), (130, 300, 768), (256, 512, 128),
+               (77, 50257, 48), (300, 96, 3072)]
+
+
+def gemm_ref(a, w, b, epi):
+    y = a.double() @ w.double().t()
+    if b is not None:
+        y = y + b.double()
+    if epi == _lib.EPI_BIAS_GELU:
+        y = R.gelu_tanh(y)
+    return y
+
+
+@pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
+@pytest.mark.parametrize("dtype", [BF16, F32])
+@pytest.mark.parametrize("epi", [_lib.EPI_NONE, _lib.EPI_BIAS, _lib.EPI_BIAS_GELU])
+def test_gemm_auto_tile(gpu, m, n, k, dtype, epi):
+    a = randn(m, k, seed=m, dtype=dtype)
+    w = randn(n, k, seed=n, dtype=dtype, scale=0.05)
+    b = None if epi == _lib.EPI_NONE else randn(n, seed=k, dtype=dtype)
+    out = cg.kernels._gemm(a.to(gpu), w.to(gpu), None if b is None else b.to(gpu), epi, F32, "t")
+    ref = gemm_ref(a, w, b, epi)
+    # fp32 accumulation of K products of |a w| ~ 0.05: error << 1e-4
+    close(out, ref, 1e-4 * math.sqrt(k / 64), 1e-5, f"gemm {dtype} {m}x{n}x{k} epi{epi}")
+
+
+@pytest.mark.parametrize("tile", range(5))
+@pytest.mark.parametrize("m,n,k", [(300, 520, 136), (512, 256, 768), (1, 50257, 64)])
+def test_gemm_every_bf16_tile(gpu, tile, m, n, k):
+    a = randn(m, k, seed=1, dtype=BF16)
+    w = randn(n, k, seed=2, dtype=BF16, scale=0.05)
+    b = randn(n, seed=3, dtype=BF16)
+    out = cg.kernels._gemm(a.to(gpu), w.to(gpu), b.to(gpu), _lib.EPI_BIAS, BF16, "t", tile=tile)
+    close(out, gemm_ref(a, w, b, _lib.EPI_BIAS), 1e-3, 2 ** -8, f"tile {tile}")
+
+
+@pytest.mark.parametrize("tile", range(2))
+def test_gemm_every_f32_tile(gpu, tile):
+    a, w = randn(200, 100, seed=4), randn(333, 100, seed=5, scale=0.1)
+    out = cg.kernels._gemm(a.to(gpu), w.to(gpu), None, _lib.EPI_NONE, F32, "t", tile=tile)
+    close(out, gemm_ref(a, w, None, 0), 1e-5, 1e-5, f"f32 tile {tile}")
+
+
+def test_gemm_strided_output_and_lda(gpu):
+    """Row-padded A (lda > K) and C written into a wider buffer (ldc > N)."""
+    lib = _lib.load()
+    m, n, k = 70, 90, 64
+    abig = randn(m, 80, seed=8, dtype=BF16).to(gpu)
+    w = randn(n, k, seed=9, dtype=BF16, scale=0.1).to(gpu)
+    c = torch.full((m, 100), 7.0, device=gpu)
+    _lib.check(lib.cgpt_gemm(abig.data_ptr(), w.data_ptr(), None, c.data_ptr(), m, n, k, 80, k,
+                             100, 1, 0, 0, 0, -1, torch.cuda.current_stream().cuda_stream), "g")
+    close(c[:, :n], gemm_ref(abig[:, :k].cpu(), w.cpu(), None, 0), 1e-4, 1e-5, "strided")
+    assert torch.all(c[:, n:] == 7.0)
+
+
+@pytest.mark.parametrize("n,k", [(2304, 768), (768, 768), (3072, 768), (768, 3072), (50257, 768)])
+def test_gemm_gpt2_shapes_vs_torch(gpu, n, k):
+    """Full GPT-2 prefill shapes (M = 16384) against torch's fp32 matmul of the
+    same bf16 operands."""
+    m = 16384
+    g = torch.Generator(device=gpu).manual_seed(n + k)
+    a = torch.randn(m, k, device=gpu, generator=g).to(BF16)
+    w = (torch.randn(n, k, device=gpu, generator=g) * 0.02).to(BF16)
+    b = torch.randn(n, device=gpu, generator=g).to(BF16)
+    out = cg.kernels._gemm(a, w, b, _lib.EPI_BIAS, F32, "t")
+    ref = torch.addmm(b.float(), a.float(), w.float().t())
+    err = (out - ref).abs().max().item()
+    assert err < 2e-4 * math.sqrt(k / 64), err
+
+
+# ---------------------------------------------------------------- Attention
+
+ATTN_SHAPES = [(1, 1, 1, 64), (1, 2, 5, 16), (2, 3, 17, 32), (1, 1, 130, 64), (2, 4, 64, 64),
+               (1, 2, 300, 128), (1, 3, 64, 16)]
+
+
+def attn_ref(q, k, v, dtype):
+    return R.causal_attention(q.double(), k.double(), v.double(),
+                              p_dtype=torch.bfloat16 if dtype == BF16 else None)
+
+
+@pytest.mark.parametrize("shape", ATTN_SHAPES)
+@pytest.mark.parametrize("dtype", [BF16, F32])
+def test_attention(gpu, shape, dtype):
+    q, k, v = (randn(*shape, seed=i, dtype=dtype) for i in range(3))
+    o = cg.cutile_causal_attention(q.to(gpu), k.to(gpu), v.to(gpu), shape[1])
+    ref = attn_ref(q, k, v, dtype)
+    if dtype == F32:
+        close(o, ref, 2e-5, 2e-5, f"attn fp32 {shape}")
+    else:
+        close(o, ref, 4e-3, 2 ** -8, f"attn bf16 {shape}")
+
+
+@pytest.mark.parametrize("dtype", [BF16, F32])
+def test_attention_standalone_config(gpu, dtype):
+    """BASELINE standalone config: B=8, H=12, T=512, hd=64, causal."""
+    shape = (8, 12, 512, 64)
+    q, k, v = (randn(*shape, seed=10 + i, dtype=dtype) for i in range(3))
+    o = cg.cutile_causal_attention(q.to(gpu), k.to(gpu), v.to(gpu), 12)
+    ref = attn_ref(q, k, v, dtype)
+    tol = (2e-5, 2e-5) if dtype == F32 else (4e-3, 2 ** -8)
+    close(o, ref, *tol, f"attn standalone {dtype}")
+
+
+def test_attention_row0_and_equal_keys(gpu):
+    shape = (1, 2, 40, 64)
+    q, k, v = (randn(*shape, seed=20 + i) for i in range(3))
+    o = cg.cutile_causal_attention(q.to(gpu), k.to(gpu), v.to(gpu), 2).cpu()
+    assert torch.equal(o[:, :, 0], v[:, :, 0])  # P = exp2(0) = 1 exactly
+    keq = k[:, :, :1].expand(shape).contiguous()
+    o2 = cg.cutile_causal_attention(q.to(gpu), keq.to(gpu), v.to(gpu), 2).cpu()
+    prefix = v.double().cumsum(2) / torch.arange(1, 41, dtype=torch.float64).view(1, 1, 40, 1)
+    close(o2, prefix, 1e-5, 1e-5, "equal keys -> prefix mean")
+
+
+@pytest.mark.parametrize("dtype", [BF16, F32])
+@pytest.mark.parametrize("B,T,H,hd", [(2, 100, 3, 16), (2, 256, 12, 64), (1, 1024, 25, 64)])
+def test_attention_qkv_layout(gpu, dtype, B, T, H, hd):
+    """Strided reads from the fused (B, T, 3D) projection, (B, T, D) output."""
+    D = H * hd
+    qkv = randn(B, T, 3 * D, seed=T, dtype=dtype)
+    o = cg.attention_qkv(qkv.to(gpu), H).cpu()
+    q, k, v = (t.reshape(B, T, H, hd).transpose(1, 2) for t in qkv.split(D, dim=2))
+    ref = attn_ref(q, k, v, dtype).transpose(1, 2).reshape(B, T, D)
+    tol = (2e-5, 2e-5) if dtype == F32 else (4e-3, 2 ** -8)
+    close(o, ref, *tol, "qkv layout")
+
+
+# ---------------------------------------------------------------- Embedding
+
+@pytest.mark.parametrize("wd,od", [(F32, F32), (BF16, F32), (BF16, BF16)])
+def test_token_pos_embedding_exact(gpu, wd, od):
+    V, BS, D = 50257, 1024, 768
+    wte, wpe = randn(V, D, seed=1, dtype=wd), randn(BS, D, seed=2, dtype=wd)
+    idx = torch.randint(0, V, (3, 77), generator=torch.Generator().manual_seed(3))
+    out = cg.token_pos_embedding(idx.to(gpu), wte.to(gpu), wpe.to(gpu), pos0=5, out_dtype=od).cpu()
+    ref = (wte.float()[idx] + wpe.float()[5:82].unsqueeze(0)).to(od)
+    assert torch.equal(out, ref)
+
+
+def test_embedding_gather_and_range_check(gpu):
+    w = randn(100, 48, seed=4)
+    idx = torch.tensor([[0, 99, 5], [7, 7, 1]])
+    out = cg.cutile_embedding(idx.to(gpu), w.to(gpu)).cpu()
+    assert torch.equal(out, w[idx])
+    with pytest.raises(IndexError):  # clamped in the kernel, reported on the host
+        cg.cutile_embedding(torch.tensor([3, 100]).to(gpu), w.to(gpu))
