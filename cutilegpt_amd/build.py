@@ -62,6 +62,12 @@ def build(verbose: bool = False, extra_flags=()) -> str:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link of libcgpt.so failed:\n{res.stderr}")
+    # Resolve every symbol now (a kernel whose host stub was not emitted shows
+    # up as an undefined symbol only at dlopen time).
+    chk = subprocess.run([sys.executable, "-c", f"import ctypes; ctypes.CDLL({tmp!r}, mode=2)"],
+                         capture_output=True, text=True)
+    if chk.returncode != 0:
+        raise RuntimeError(f"libcgpt.so does not load:\n{chk.stderr}")
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")

@@ -85,15 +85,16 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // tanh-approximate GELU written through the identity
 //   0.5 x (1 + tanh(u)) = x / (1 + exp(-2u)),  u = sqrt(2/pi) (x + 0.044715 x^3),
-// with exp(-2u) = 2^(-2u log2 e) on the hardware exp2.  Saturates cleanly:
-// u -> +inf gives x, u -> -inf gives -0.
+// with exp(-2u) = 2^(-2u log2 e) on the hardware exp2 and the reciprocal on the
+// hardware v_rcp_f32 (1 ulp).  Saturates cleanly: u -> +inf gives x, u -> -inf
+// gives -0 (rcp(inf) = 0).
 __device__ __forceinline__ float gelu_tanh(float x) {
   constexpr float kSqrt2OverPi = 0.7978845608028654f;
   constexpr float kCoef = 0.044715f;
   constexpr float kNeg2Log2e = -2.8853900817779268f;  // -2 / ln 2
   float u = kSqrt2OverPi * (x + kCoef * x * x * x);
   float e = __builtin_amdgcn_exp2f(kNeg2Log2e * u);
-  return x / (1.0f + e);
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 // Error codes shared with the C ABI (see include/cgpt.h).

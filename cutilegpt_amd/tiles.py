@@ -7,8 +7,15 @@ fp16) and the unwired ``TileConfig`` (``cutile_gpt/api/config.py:36-64``).
 Tile ids index the configuration table compiled into libcgpt.so
 (``csrc/gemm.hip``):
 
-    bf16: 0 = 256x256 (4 waves, 128x128 each), 1 = 256x128, 2 = 128x128,
+    bf16, register-staged double buffer:
+          0 = 256x256 (4 waves, 128x128 each), 1 = 256x128, 2 = 128x128,
           3 = 128x64, 4 = 64x64
+    bf16, direct-to-LDS pipeline (K % 64 == 0):
+          5 = 256x128 (4 waves), 6 = 256x128 (8 waves), 7 = 128x256 (8 waves),
+          8 = 128x128 (4 waves), all 3 stages; 9 = 256x256 (8 waves, 128x64
+          each), 10 = 256x256 (4 waves), 2 stages
+    bf16, persistent direct-to-LDS (one block per CU, K % 64 == 0, K >= 128):
+          11 = 256x128 (8 waves), 12 = 128x256 (8 waves), 3 stages
     fp32: 0 = 128x128, 1 = 64x64
 
 ``TABLE`` maps exact (dtype, M, N, K) problems measured on MI355X to the tile
@@ -22,8 +29,22 @@ from typing import Dict, Tuple
 
 from . import _lib
 
-# (dtype code, M, N, K) -> tile id.  Filled from rocprofv3 sweeps on MI355X.
-TABLE: Dict[Tuple[int, int, int, int], int] = {}
+# (dtype code, M, N, K) -> tile id.  Winners of an event-timed sweep of every
+# tile on MI355X (bias epilogue, bf16 out); TFLOP/s of the winner in comments.
+_B = _lib.CGPT_BF16
+TABLE: Dict[Tuple[int, int, int, int], int] = {
+    # GPT-2 124M prefill, M = 16 x 1024
+    (_B, 16384, 2304, 768): 11,   # c_attn      594
+    (_B, 16384, 768, 768): 12,    # attn c_proj 493
+    (_B, 16384, 3072, 768): 12,   # c_fc        651
+    (_B, 16384, 768, 3072): 9,    # mlp c_proj  828
+    (_B, 16384, 50257, 768): 9,   # lm head     646 (fp32 logits)
+    # 'medium' (8L, d 512) prefill, M = 16 x 256
+    (_B, 4096, 1536, 512): 11,    # 358
+    (_B, 4096, 2048, 512): 11,    # 451
+    (_B, 4096, 512, 2048): 3,     # 271
+    (_B, 4096, 50257, 512): 12,   # 376
+}
 
 
 def gemm_tile(dtype_code: int, m: int, n: int, k: int) -> int:

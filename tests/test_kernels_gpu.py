@@ -131,6 +131,54 @@ def test_gemm_every_bf16_tile(gpu, tile, m, n, k):
     close(out, gemm_ref(a, w, b, _lib.EPI_BIAS), 1e-3, 2 ** -8, f"tile {tile}")
 
 
+DMA_TILES = [5, 6, 7, 8, 9, 10]
+
+
+@pytest.mark.parametrize("tile", DMA_TILES)
+@pytest.mark.parametrize("m,n,k", [(300, 520, 192), (512, 256, 768), (1, 50257, 64),
+                                   (257, 129, 128), (1000, 3072, 1600)])
+@pytest.mark.parametrize("epi", [_lib.EPI_NONE, _lib.EPI_BIAS_GELU])
+def test_gemm_dma_tiles(gpu, tile, m, n, k, epi):
+    """Direct-to-LDS pipeline (K % 64 == 0): ragged M/N edges, 1..25 K steps."""
+    a = randn(m, k, seed=11, dtype=BF16)
+    w = randn(n, k, seed=12, dtype=BF16, scale=0.05)
+    b = randn(n, seed=13, dtype=BF16)
+    out = cg.kernels._gemm(a.to(gpu), w.to(gpu), b.to(gpu), epi, F32, "t", tile=tile)
+    ref = gemm_ref(a, w, None if epi == _lib.EPI_NONE else b, epi)
+    close(out, ref, 1e-4 * math.sqrt(k / 64), 1e-5, f"dma tile {tile} {m}x{n}x{k}")
+
+
+PERSIST_TILES = [11, 12]
+
+
+@pytest.mark.parametrize("tile", PERSIST_TILES)
+@pytest.mark.parametrize("m,n,k", [(300, 520, 128), (4096, 4096, 256), (257, 50257, 192),
+                                   (16384, 768, 3072), (1, 3, 128)])
+@pytest.mark.parametrize("epi", [_lib.EPI_BIAS, _lib.EPI_BIAS_GELU])
+def test_gemm_persistent_tiles(gpu, tile, m, n, k, epi):
+    """Persistent kernel: several tiles per block (tile boundaries inside the
+    flattened K stream), fewer tiles than CUs, ragged edges."""
+    a = randn(m, k, seed=21, dtype=BF16)
+    w = randn(n, k, seed=22, dtype=BF16, scale=0.05)
+    b = randn(n, seed=23, dtype=BF16)
+    out = cg.kernels._gemm(a.to(gpu), w.to(gpu), b.to(gpu), epi, BF16, "t", tile=tile)
+    ref = gemm_ref(a, w, b, epi)
+    close(out, ref, 2e-3, 2 ** -8, f"persistent tile {tile} {m}x{n}x{k}")
+
+
+def test_gemm_persistent_rejects_single_k_step(gpu):
+    a = randn(64, 64, dtype=BF16).to(gpu)
+    with pytest.raises(ValueError):
+        cg.kernels._gemm(a, a, None, _lib.EPI_NONE, F32, "t", tile=11)
+
+
+def test_gemm_dma_rejects_ragged_k(gpu):
+    a = randn(64, 72, dtype=BF16).to(gpu)
+    w = randn(64, 72, dtype=BF16).to(gpu)
+    with pytest.raises(ValueError):
+        cg.kernels._gemm(a, w, None, _lib.EPI_NONE, F32, "t", tile=5)
+
+
 @pytest.mark.parametrize("tile", range(2))
 def test_gemm_every_f32_tile(gpu, tile):
     a, w = randn(200, 100, seed=4), randn(333, 100, seed=5, scale=0.1)
