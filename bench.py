@@ -33,6 +33,10 @@ if ROOT not in sys.path:
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+# Bytes beyond L2 per LM-head launch (2.0 x FETCH_SIZE + 1.0 x WRITE_SIZE, factors from
+# a 1 GiB copy), measured with rocprofv3 --pmc on the GPT-2 workload; see
+# profiles/lm_head_gemm_gpt2_traffic_pmc.md.  Only valid for the gpt2 workload.
+LM_HEAD_TRAFFIC_BYTES = 5.27e9
 
 WORKLOADS = {
     "gpt2": dict(n_layer=12, n_head=12, n_embd=768, batch=16, seq=1024,
@@ -59,6 +63,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seqs", type=int, default=2,
                     help="sequences (of seq_len tokens) per timed CPU-baseline forward")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="after the run, copy a buffer of this many MiB 3 times (a kernel of "
+                         "known traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -165,6 +172,15 @@ def main():
         breakdown[tag] = {"ms": round(ms, 4), "launches": n, unit: round(rate, 1),
                           "frac": round(rate / peak, 4)}
 
+    if args.calib_copy_mib > 0:
+        n = args.calib_copy_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(w, ids, H, args.cpu_seqs)
@@ -188,7 +204,8 @@ def main():
         "roofline": {"bound": "mfma", "kernel": "lm_head GEMM (gemm_kernel bf16, N=50257, K=768)",
                      "achieved": round(head_tflops, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(head_tflops / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None, "avg_launch_ms": round(head_avg_ms, 4)},
+                     "traffic": LM_HEAD_TRAFFIC_BYTES if args.workload == "gpt2" else None,
+                     "avg_launch_ms": round(head_avg_ms, 4)},
         "forward_tflops": round((gemm_f + head_f + attn_f) / (ms_per_step * 1e-3) / 1e12, 1),
         "breakdown": breakdown,
         "cpu_baseline": cpu,
