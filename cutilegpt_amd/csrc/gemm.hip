@@ -1,11 +1,11 @@
 // C[M,N] = epilogue(A[M,K] W[N,K]^T + bias) on CDNA4 matrix cores.
 //
-// Layout and schedule
+// Layout shared by every kernel in this file
 //  * A (activations, row-major) and W (nn.Linear weight, row-major (N, K)) are
-//    both K-contiguous, so both tiles are staged in LDS the same way: one
-//    128-byte LDS row per matrix row per K step (64 bf16 or 32 fp32), written
-//    as eight 16-byte chunks whose position is XOR-swizzled with (row & 7) to
-//    spread the fragment reads of 16 consecutive rows over the LDS banks.
+//    both K-contiguous, so both tiles are staged in LDS the same way: one LDS
+//    row per matrix row per stage (64 or 128 bytes of K), made of 16-byte chunks
+//    whose position is XOR-swizzled with the row index so that the fragment
+//    reads of 16 consecutive rows hit distinct LDS banks.
 //  * A block of WGM x WGN wavefronts owns a BM x BN output tile; each wave owns
 //    a (BM/WGM) x (BN/WGN) sub-tile made of 16x16 MFMA tiles.  The MFMA is fed
 //    with the W fragment as its "A" operand and the activation fragment as its
@@ -16,11 +16,15 @@
 //    fp32: four v_mfma_f32_16x16x4_f32 per 16-byte fragment; lane group g
 //    supplies k = 4g + j to the j-th MFMA (any consistent permutation of the
 //    k axis leaves the dot product unchanged).
-//  * Global -> register -> LDS double buffering: the loads of K step t+1 are in
-//    flight while the MFMAs of step t run; one barrier per K step.
-//  * Block ids are remapped so that tiles adjacent in the grouped (GROUP_M)
-//    order run on the same XCD (the dispatcher deals block ids round-robin over
-//    the 8 XCDs, each with its own L2).
+//  * Block (or tile) ids are remapped so that tiles adjacent in the grouped
+//    (GROUP_M) order run on the same XCD (the dispatcher deals block ids
+//    round-robin over the 8 XCDs, each with its own L2).
+//
+// Two main loops:
+//  * gemm_kernel: global -> registers -> LDS double buffering (fp32, and small
+//    bf16 problems, any K multiple of 8/4).
+//  * gemm_pipe_kernel: bf16 direct-to-LDS multi-stage pipeline, persistent
+//    over tiles (see the comment above it).
 #include "common.h"
 
 namespace cgpt {
@@ -54,7 +58,8 @@ __device__ __forceinline__ float load_bias(const void* bias, bool bf16, int64_t 
   return bf16 ? bf16_to_f32(static_cast<const bf16_t*>(bias)[n]) : static_cast<const float*>(bias)[n];
 }
 
-// Map a hardware block id to (tile_m, tile_n): XCD-contiguous, then grouped.
+// Map a hardware block (or persistent tile) id to (tile_m, tile_n):
+// XCD-contiguous ranges of logical tiles, then groups of kGroupM tile rows.
 __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
   const int nblocks = tiles_m * tiles_n;
   const int q = nblocks / kNumXcd, r = nblocks % kNumXcd;
@@ -68,6 +73,35 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
   tm = first_m + in_group % gsz;
   tn = in_group / gsz;
 }
+
+// Per-wave LDS scratch for re-mapping one 16x16 output block (17-float rows:
+// conflict-free column and row accesses).
+constexpr int kScrFloats = 16 * 17;
+
+// Store a 16x16 block held in the C^T accumulator layout (lane l: row l%16,
+// columns 4(l/16)..+3, values v[0..3]) when rows cannot take 16-byte stores
+// (ldc not a multiple of 4, e.g. a 50257-wide vocabulary).  The block goes
+// through the wave's LDS scratch so that each store instruction writes 16
+// consecutive columns of 4 rows instead of 16 scattered rows.
+template <typename TOut>
+__device__ __forceinline__ void store_block_remap(float* scr, TOut* __restrict__ C, int64_t ldc,
+                                                  int m0, int n0, int M, int N, const float* v,
+                                                  int lane) {
+  const int c = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) scr[c * 17 + 4 * g + r] = v[r];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = 4 * g + r;
+    const float x = scr[row * 17 + c];
+    const int m = m0 + row, n = n0 + c;
+    if (m < M && n < N) Elem<TOut>::store(C + static_cast<int64_t>(m) * ldc + n, x);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Register-staged double-buffered kernel (fp32 and bf16; K % 8 (bf16) or
+// K % 4 (fp32); the K tail of the last 128-byte row is zero-filled).
 
 template <typename TIn, int BM, int BN, int WGM, int WGN, int EPI, typename TOut>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(
@@ -206,50 +240,35 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// bf16 GEMM with a 3-stage direct-to-LDS pipeline (K % 64 == 0).
+// bf16 direct-to-LDS pipeline, persistent over tiles.
 //
-// Tiles reach LDS through `buffer_load_dwordx4 ... lds`: each lane's 16 bytes
-// land at (LDS base + lane * 16), so one wave instruction fills 8 LDS rows of
-// 128 bytes; the XOR swizzle is applied on the global side (the lane that
-// fills physical chunk p of row r fetches logical chunk p ^ (r & 7)).  No
-// staging registers and no ds_write.  Per-lane byte offsets into A and W are
-// loop-invariant; the K advance is the scalar offset.  Rows past M (or N) are
-// clamped to the last row, so every access stays inside the matrix (those
-// rows only feed outputs that are never stored).
-//
-// Stage k+2 is issued while stage k is computed; before computing stage k each
-// wave waits until at most one stage (k+1) of its own DMA is still in flight
-// (s_waitcnt vmcnt), then a raw s_barrier publishes every wave's part.  A full
-// __syncthreads would add a release fence, i.e. vmcnt(0), and collapse the
-// pipeline to one stage.  The empty asm statements keep the compiler from
-// moving LDS accesses across the barrier.
+// * Tiles reach LDS through `buffer_load_dwordx4 ... lds`: each lane's 16 bytes
+//   land at (LDS base + lane * 16), so one wave instruction fills 1 KiB of LDS
+//   rows; the XOR swizzle is applied on the global side (the lane that fills
+//   physical chunk p of row r fetches logical chunk p ^ swz(r)).  No staging
+//   registers and no ds_write.  Per-lane byte offsets are loop-invariant
+//   within a tile; the K advance is the scalar offset.  Rows past M (or N) are
+//   clamped to the last row, so every access stays inside the matrix.
+// * A stage holds SPS k32 slabs (LDS rows of 64 * SPS bytes); STAGES stages
+//   rotate through distinct __shared__ arrays.  Stage g + STAGES - 1 is issued
+//   right after the barrier of step g; before that barrier each wave waits
+//   (s_waitcnt vmcnt) until only its own later stages are still in flight, then
+//   a raw s_barrier publishes every wave's part.  A full __syncthreads would
+//   add a release fence, i.e. vmcnt(0), and collapse the pipeline to one stage;
+//   the empty asm statements keep the compiler from moving LDS accesses across
+//   the barrier, and lgkmcnt(0) in the same wait retires the previous stage's
+//   LDS reads before its buffer is refilled.
+// * Fragment reads are software-pipelined: the slab read after a barrier
+//   overlaps the MFMAs of the previous slab (held in the other fragment set).
+// * Persistent: block b walks tiles b, b + grid, ...; their K stages form one
+//   flattened stream, so the first stages of tile i+1 are in flight while tile
+//   i finishes.  A tile's bias is fetched right after the barrier of its last
+//   step (before that step's DMA), so the epilogue one step later finds it in
+//   registers without draining the DMA queue; the step after an epilogue waits
+//   for every outstanding transfer (its stores count in vmcnt too).
+// Requires K % (32 * SPS) == 0.
 
 #define CGPT_LDS(p) ((__attribute__((address_space(3))) void*)(p))
-
-// Per-wave LDS scratch for re-mapping one 16x16 output block (17-float rows:
-// conflict-free column and row accesses).
-constexpr int kScrFloats = 16 * 17;
-
-// Store a 16x16 block held in the C^T accumulator layout (lane l: row l%16,
-// columns 4(l/16)..+3, values v[0..3]) when rows cannot take 16-byte stores
-// (ldc not a multiple of 4, e.g. a 50257-wide vocabulary).  The block goes
-// through the wave's LDS scratch so that each store instruction writes 16
-// consecutive columns of 4 rows instead of 16 scattered rows.
-template <typename TOut>
-__device__ __forceinline__ void store_block_remap(float* scr, TOut* __restrict__ C, int64_t ldc,
-                                                  int m0, int n0, int M, int N, const float* v,
-                                                  int lane) {
-  const int c = lane & 15, g = lane >> 4;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) scr[c * 17 + 4 * g + r] = v[r];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int row = 4 * g + r;
-    const float x = scr[row * 17 + c];
-    const int m = m0 + row, n = n0 + c;
-    if (m < M && n < N) Elem<TOut>::store(C + static_cast<int64_t>(m) * ldc + n, x);
-  }
-}
 
 __device__ __forceinline__ void raw_barrier() {
   asm volatile("" ::: "memory");
@@ -258,19 +277,28 @@ __device__ __forceinline__ void raw_barrier() {
 }
 
 // s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt[3:0], expcnt[6:4],
-// lgkmcnt[11:8], vmcnt[5:4] at [15:14]).  lgkmcnt(0) also guarantees that no
-// LDS read of the previous stage is still in flight when the barrier lets
-// another wave's DMA reuse that buffer.
+// lgkmcnt[11:8], vmcnt[5:4] at [15:14]).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
 }
 
+// Wait until at most `later` stages of LPS loads each are in flight.
+template <int LPS, int MAXLATER>
+__device__ __forceinline__ void wait_stages(int later) {
+  static_assert(MAXLATER <= 4, "up to 6 stages");
+  if (MAXLATER >= 4 && later >= 4) { wait_vmcnt<4 * LPS>(); return; }
+  if (MAXLATER >= 3 && later >= 3) { wait_vmcnt<3 * LPS>(); return; }
+  if (MAXLATER >= 2 && later >= 2) { wait_vmcnt<2 * LPS>(); return; }
+  if (MAXLATER >= 1 && later >= 1) { wait_vmcnt<1 * LPS>(); return; }
+  wait_vmcnt<0>();
+}
+
 constexpr uint32_t kBufferRsrcWord3 = 0x00020000u;  // raw buffer, gfx9 family
 
-template <int BM, int BN, int WGM, int WGN, int STAGES, int EPI, typename TOut>
-__global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(
+template <int BM, int BN, int WGM, int WGN, int SPS, int STAGES, int EPI, typename TOut>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
     const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, const void* __restrict__ bias,
     bool bias_bf16, TOut* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldw,
     int64_t ldc, int tiles_m, int tiles_n, bool vec_store) {
@@ -280,179 +308,31 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(
   constexpr int NT = 64 * WGM * WGN, NW = NT / 64;
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 16, TN = WN / 16;
-  constexpr int STAGE = (BM + BN) * 128;
-  constexpr int A_INS = BM / (8 * NW);  // DMA instructions per wave per stage (8 rows each)
-  constexpr int W_INS = BN / (8 * NW);
-  constexpr int LPS = A_INS + W_INS;    // loads per wave per stage
-  static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "tile/wave mismatch");
+  constexpr int ROWB = 64 * SPS;           // bytes of K per LDS row per stage
+  constexpr int CPR = ROWB / 16;           // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;            // rows filled by one wave DMA instruction
+  constexpr int STAGE = (BM + BN) * ROWB;
+  constexpr int A_INS = BM / (RPI * NW);
+  constexpr int W_INS = BN / (RPI * NW);
+  constexpr int LPS = A_INS + W_INS;       // DMA instructions per wave per stage
+  static_assert(SPS == 1 || SPS == 2, "one or two k32 slabs per stage");
+  static_assert(STAGES >= 2 && STAGES <= 6, "2..6 stages");
+  static_assert(SPS == 2 || STAGES % 2 == 0, "single-slab stages alternate fragment sets");
+  static_assert(BM % (RPI * NW) == 0 && BN % (RPI * NW) == 0, "tile/wave mismatch");
+  static_assert((STAGES - 2) * LPS < 64, "vmcnt range");
   __shared__ __attribute__((aligned(1024))) uint8_t st0[STAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t st1[STAGE];
-  __shared__ __attribute__((aligned(1024))) uint8_t st2[STAGES == 3 ? STAGE : 16];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
-  int tile_m, tile_n;
-  tile_coords(blockIdx.x, tiles_m, tiles_n, tile_m, tile_n);
-  const int m0 = tile_m * BM, n0 = tile_n * BN;
-
-  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<bf16_t*>(A), 0, static_cast<int>(static_cast<int64_t>(M) * lda * 2), kBufferRsrcWord3);
-  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<bf16_t*>(W), 0, static_cast<int>(static_cast<int64_t>(N) * ldw * 2), kBufferRsrcWord3);
-  const int lrow = lane >> 3, pchunk = lane & 7;
-  uint32_t aoff[A_INS], woff[W_INS];
-#pragma unroll
-  for (int i = 0; i < A_INS; ++i) {
-    const int row = (i * NW + wave) * 8 + lrow;
-    const int64_t g = min(m0 + row, M - 1);
-    aoff[i] = static_cast<uint32_t>(g * lda * 2 + ((pchunk ^ (row & 7)) << 4));
-  }
-#pragma unroll
-  for (int i = 0; i < W_INS; ++i) {
-    const int row = (i * NW + wave) * 8 + lrow;
-    const int64_t g = min(n0 + row, N - 1);
-    woff[i] = static_cast<uint32_t>(g * ldw * 2 + ((pchunk ^ (row & 7)) << 4));
-  }
-  auto issue = [&](uint8_t* buf, int kt) {
-    const int soff = kt * 128;
-#pragma unroll
-    for (int i = 0; i < A_INS; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, CGPT_LDS(buf + (i * NW + wave) * 1024), 16,
-                                               aoff[i], soff, 0, 0);
-#pragma unroll
-    for (int i = 0; i < W_INS; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, CGPT_LDS(buf + BM * 128 + (i * NW + wave) * 1024),
-                                               16, woff[i], soff, 0, 0);
-  };
-
-  f32x4_t acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  const int frow = lane & 15, fgrp = lane >> 4;
-  // Byte offset of this lane's fragment row inside a stage, per k32 slab.
-  const int xo0 = ((fgrp ^ (frow & 7)) << 4), xo1 = (((4 + fgrp) ^ (frow & 7)) << 4);
-  const int a_base = (wm0 + frow) * 128, w_base = BM * 128 + (wn0 + frow) * 128;
-  // Fragments of one k32 slab: TM activation and TN weight 16-byte reads.
-  struct Frag {
-    u32x4_t a[TM], w[TN];
-  };
-  auto read_slab = [&](const uint8_t* buf, int xo, Frag& f) {
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-      f.a[i] = *reinterpret_cast<const u32x4_t*>(buf + a_base + i * 16 * 128 + xo);
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-      f.w[j] = *reinterpret_cast<const u32x4_t*>(buf + w_base + j * 16 * 128 + xo);
-  };
-  auto mma_slab = [&](const Frag& f) {
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) Mfma<bf16_t>::run(f.w[j], f.a[i], acc[i][j]);
-  };
-
-  // Software pipeline across the barrier: after the barrier of step kt, slab 0
-  // of stage kt is read from LDS while the MFMAs of slab 1 of stage kt-1 (already
-  // in registers) run, then slab 1 of stage kt is read while slab 0's MFMAs run.
-  const int KT = K / 64;
-  Frag f0, f1;
-  auto step = [&](uint8_t* cur, uint8_t* dst, int kt, bool first) {
-    if constexpr (STAGES == 3) {
-      if (kt + 1 < KT) wait_vmcnt<LPS>();
-      else wait_vmcnt<0>();
-    } else {
-      wait_vmcnt<0>();
-    }
-    raw_barrier();
-    if (kt + STAGES - 1 < KT) issue(dst, kt + STAGES - 1);
-    read_slab(cur, xo0, f0);
-    if (!first) mma_slab(f1);
-    read_slab(cur, xo1, f1);
-    mma_slab(f0);
-  };
-
-  uint8_t* bufs[3] = {st0, st1, st2};
-#pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s)
-    if (s < KT) issue(bufs[s], s);
-  step(bufs[0], bufs[STAGES - 1], 0, true);
-  for (int kt = 1; kt < KT; kt += STAGES) {
-#pragma unroll
-    for (int j = 0; j < STAGES; ++j)
-      if (kt + j < KT) step(bufs[(1 + j) % STAGES], bufs[j % STAGES], kt + j, false);
-  }
-  mma_slab(f1);
-
+  __shared__ __attribute__((aligned(1024))) uint8_t st2[STAGES > 2 ? STAGE : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t st3[STAGES > 3 ? STAGE : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t st4[STAGES > 4 ? STAGE : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t st5[STAGES > 5 ? STAGE : 16];
   __shared__ float escr[NW][kScrFloats];
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int mb = m0 + wm0 + i * 16;
-    const int m = mb + frow;
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int nb = n0 + wn0 + j * 16;
-      const int n = nb + 4 * fgrp;
-      float v[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float t = acc[i][j][r];
-        if (EPI != CGPT_EPI_NONE && n + r < N) t += load_bias(bias, bias_bf16, n + r);
-        if (EPI == CGPT_EPI_BIAS_GELU) t = gelu_tanh(t);
-        v[r] = t;
-      }
-      if (!vec_store) {
-        store_block_remap(escr[wave], C, ldc, mb, nb, M, N, v, lane);
-      } else if (m < M && n < N) {
-        TOut* out = C + static_cast<int64_t>(m) * ldc + n;
-        if (n + 3 < N) {
-          store4_out(out, v);
-        } else {
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (n + r < N) Elem<TOut>::store(out + r, v[r]);
-        }
-      }
-    }
-  }
-#endif  // __HIP_DEVICE_COMPILE__
-}
-
-// ---------------------------------------------------------------------------
-// Persistent bf16 GEMM: one block per CU walks the tiles
-// t = blockIdx.x + i * gridDim.x (in the XCD-aware grouped order) and runs
-// their K steps as one flattened stream through the same direct-to-LDS
-// pipeline, so the first stages of tile i+1 are already in flight while tile i
-// finishes and runs its epilogue.  The bias of a tile is fetched right after
-// the barrier of its last K step (before that step's DMA is issued), so the
-// epilogue one step later finds it in registers without draining the DMA
-// queue.  The step after an epilogue waits for every outstanding transfer
-// (its stores are counted by vmcnt too).  Requires K % 64 == 0 and K >= 128.
-
-template <int BM, int BN, int WGM, int WGN, int STAGES, int EPI, typename TOut>
-__global__ __launch_bounds__(64 * WGM * WGN) void gemm_persist_kernel(
-    const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, const void* __restrict__ bias,
-    bool bias_bf16, TOut* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldw,
-    int64_t ldc, int tiles_m, int tiles_n, bool vec_store) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  constexpr int NT = 64 * WGM * WGN, NW = NT / 64;
-  constexpr int WM = BM / WGM, WN = BN / WGN;
-  constexpr int TM = WM / 16, TN = WN / 16;
-  constexpr int STAGE = (BM + BN) * 128;
-  constexpr int A_INS = BM / (8 * NW);
-  constexpr int W_INS = BN / (8 * NW);
-  constexpr int LPS = A_INS + W_INS;
-  static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "tile/wave mismatch");
-  __shared__ __attribute__((aligned(1024))) uint8_t st0[STAGE];
-  __shared__ __attribute__((aligned(1024))) uint8_t st1[STAGE];
-  __shared__ __attribute__((aligned(1024))) uint8_t st2[STAGES == 3 ? STAGE : 16];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
   const int frow = lane & 15, fgrp = lane >> 4;
-  const int lrow = lane >> 3, pchunk = lane & 7;
+  const int lrow = lane / CPR, pchunk = lane % CPR;
+  auto swz = [](int row) { return ROWB == 128 ? (row & 7) : ((row >> 1) & 3); };
 
   const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<bf16_t*>(A), 0, static_cast<int>(static_cast<int64_t>(M) * lda * 2), kBufferRsrcWord3);
@@ -460,11 +340,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_persist_kernel(
       const_cast<bf16_t*>(W), 0, static_cast<int>(static_cast<int64_t>(N) * ldw * 2), kBufferRsrcWord3);
 
   const int n_tiles = tiles_m * tiles_n;
-  const int KT = K / 64;
+  const int KT = K / (32 * SPS);
   const int n_mine = (n_tiles - 1 - static_cast<int>(blockIdx.x)) / static_cast<int>(gridDim.x) + 1;
   const int total = n_mine * KT;
 
-  // ---- issue side: the next flattened step to fetch and its tile's offsets
+  // ---- issue side: next flattened stage to fetch and its tile's offsets
   int iss_i = 0, iss_kt = 0;
   uint32_t aoff[A_INS], woff[W_INS];
   auto set_offsets = [&](int i) {
@@ -474,26 +354,26 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_persist_kernel(
     const int m0 = tm * BM, n0 = tn * BN;
 #pragma unroll
     for (int ii = 0; ii < A_INS; ++ii) {
-      const int row = (ii * NW + wave) * 8 + lrow;
+      const int row = (ii * NW + wave) * RPI + lrow;
       const int64_t g = min(m0 + row, M - 1);
-      aoff[ii] = static_cast<uint32_t>(g * lda * 2 + ((pchunk ^ (row & 7)) << 4));
+      aoff[ii] = static_cast<uint32_t>(g * lda * 2 + ((pchunk ^ swz(row)) << 4));
     }
 #pragma unroll
     for (int ii = 0; ii < W_INS; ++ii) {
-      const int row = (ii * NW + wave) * 8 + lrow;
+      const int row = (ii * NW + wave) * RPI + lrow;
       const int64_t g = min(n0 + row, N - 1);
-      woff[ii] = static_cast<uint32_t>(g * ldw * 2 + ((pchunk ^ (row & 7)) << 4));
+      woff[ii] = static_cast<uint32_t>(g * ldw * 2 + ((pchunk ^ swz(row)) << 4));
     }
   };
   auto issue = [&](uint8_t* buf) {
-    const int soff = iss_kt * 128;
+    const int soff = iss_kt * ROWB;
 #pragma unroll
     for (int ii = 0; ii < A_INS; ++ii)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, CGPT_LDS(buf + (ii * NW + wave) * 1024), 16,
                                                aoff[ii], soff, 0, 0);
 #pragma unroll
     for (int ii = 0; ii < W_INS; ++ii)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, CGPT_LDS(buf + BM * 128 + (ii * NW + wave) * 1024),
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, CGPT_LDS(buf + BM * ROWB + (ii * NW + wave) * 1024),
                                                16, woff[ii], soff, 0, 0);
     if (++iss_kt == KT) {
       iss_kt = 0;
@@ -509,18 +389,21 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_persist_kernel(
 #pragma unroll
       for (int j = 0; j < TN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   };
-  const int xo0 = ((fgrp ^ (frow & 7)) << 4), xo1 = (((4 + fgrp) ^ (frow & 7)) << 4);
-  const int a_base = (wm0 + frow) * 128, w_base = BM * 128 + (wn0 + frow) * 128;
+  // Byte offset of this lane's fragment row inside a stage, per slab.
+  int xo[SPS];
+#pragma unroll
+  for (int s = 0; s < SPS; ++s) xo[s] = ((4 * s + fgrp) ^ swz(frow)) << 4;
+  const int a_base = (wm0 + frow) * ROWB, w_base = BM * ROWB + (wn0 + frow) * ROWB;
   struct Frag {
     u32x4_t a[TM], w[TN];
   };
-  auto read_slab = [&](const uint8_t* buf, int xo, Frag& f) {
+  auto read_slab = [&](const uint8_t* buf, int s, Frag& f) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
-      f.a[i] = *reinterpret_cast<const u32x4_t*>(buf + a_base + i * 16 * 128 + xo);
+      f.a[i] = *reinterpret_cast<const u32x4_t*>(buf + a_base + i * 16 * ROWB + xo[s]);
 #pragma unroll
     for (int j = 0; j < TN; ++j)
-      f.w[j] = *reinterpret_cast<const u32x4_t*>(buf + w_base + j * 16 * 128 + xo);
+      f.w[j] = *reinterpret_cast<const u32x4_t*>(buf + w_base + j * 16 * ROWB + xo[s]);
   };
   auto mma_slab = [&](const Frag& f) {
 #pragma unroll
@@ -529,7 +412,6 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_persist_kernel(
       for (int j = 0; j < TN; ++j) Mfma<bf16_t>::run(f.w[j], f.a[i], acc[i][j]);
   };
 
-  // Bias of the tile being finished: 4 consecutive columns per 16-wide j block.
   f32x4_t bval[TN];
   auto load_bias_tile = [&](int i) {
     int tm, tn;
@@ -563,9 +445,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_persist_kernel(
           if (EPI == CGPT_EPI_BIAS_GELU) t = gelu_tanh(t);
           v[r] = t;
         }
-        if (m < M && n < N) {
+        if (!vec_store) {
+          store_block_remap(escr[wave], C, ldc, mb, nb, M, N, v, lane);
+        } else if (m < M && n < N) {
           TOut* out = C + static_cast<int64_t>(m) * ldc + n;
-          if (vec_store && n + 3 < N) {
+          if (n + 3 < N) {
             store4_out(out, v);
           } else {
 #pragma unroll
@@ -577,32 +461,59 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_persist_kernel(
     }
   };
 
-  Frag f0, f1;
+  // With one wave per SIMD (4-wave blocks) fragment reads are double-buffered
+  // across slabs so a wave overlaps its own LDS reads with its MFMAs; with two
+  // waves per SIMD the other wave covers that latency and a single fragment
+  // set keeps the register budget (256 per wave) free of spills.
+  constexpr bool kDB = NW == 4;
+  Frag fr[kDB ? 2 : 1];
   int cmp_i = 0, cmp_kt = 0;
   bool after_epi = false;
-  auto step = [&](const uint8_t* cur, uint8_t* dst, int g) {
-    if constexpr (STAGES == 3) {
-      if (!after_epi && g + 1 < total) wait_vmcnt<LPS>();
-      else wait_vmcnt<0>();
-    } else {
-      wait_vmcnt<0>();
-    }
+  // One flattened step g on stage buffer `cur`; `dst` receives stage g+STAGES-1.
+  // Double-buffered: slab q of the stream (q = g*SPS + s) is read into
+  // fr[q % 2] while the MFMAs of slab q-1 run from fr[(q-1) % 2] (with SPS == 1
+  // the parity is j % 2), and a tile's epilogue runs at the next tile's first
+  // step.  Single set: read slab, MFMA slab; the epilogue ends the tile's last
+  // step.
+  auto step = [&](const uint8_t* cur, uint8_t* dst, int g, int j) {
+    int later = total - 1 - g;
+    later = later < STAGES - 2 ? later : STAGES - 2;
+    if (after_epi) later = 0;
+    wait_stages<LPS, STAGES - 2>(later);
     raw_barrier();
     after_epi = false;
-    if (EPI != CGPT_EPI_NONE && cmp_kt == KT - 1) load_bias_tile(cmp_i);
+    const bool last = cmp_kt == KT - 1;
+    if (EPI != CGPT_EPI_NONE && last) load_bias_tile(cmp_i);
     if (g + STAGES - 1 < total) issue(dst);
-    if (cmp_kt == 0 && g > 0) {
-      mma_slab(f1);
-      epilogue(cmp_i - 1);
-      zero_acc();
-      after_epi = true;
-      read_slab(cur, xo0, f0);
+    if constexpr (kDB) {
+#pragma unroll
+      for (int s = 0; s < SPS; ++s) {
+        const int p = SPS == 2 ? s : (j & 1);
+        Frag& now = fr[p];
+        Frag& prev = fr[p ^ 1];
+        if (s == 0 && cmp_kt == 0 && g > 0) {
+          mma_slab(prev);
+          epilogue(cmp_i - 1);
+          zero_acc();
+          after_epi = true;
+          read_slab(cur, s, now);
+        } else {
+          read_slab(cur, s, now);
+          if (g > 0 || s > 0) mma_slab(prev);
+        }
+      }
     } else {
-      read_slab(cur, xo0, f0);
-      if (g > 0) mma_slab(f1);
+#pragma unroll
+      for (int s = 0; s < SPS; ++s) {
+        read_slab(cur, s, fr[0]);
+        mma_slab(fr[0]);
+      }
+      if (last) {
+        epilogue(cmp_i);
+        zero_acc();
+        after_epi = true;
+      }
     }
-    read_slab(cur, xo1, f1);
-    mma_slab(f0);
     if (++cmp_kt == KT) {
       cmp_kt = 0;
       ++cmp_i;
@@ -611,50 +522,53 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_persist_kernel(
 
   zero_acc();
   set_offsets(0);
-  auto bufp = [&](int j) -> uint8_t* { return j == 0 ? st0 : (j == 1 ? st1 : st2); };
+  auto bufp = [&](int b) -> uint8_t* {
+    return b == 0 ? st0 : b == 1 ? st1 : b == 2 ? st2 : b == 3 ? st3 : b == 4 ? st4 : st5;
+  };
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
     if (s < total) issue(bufp(s));
   for (int g0 = 0; g0 < total; g0 += STAGES) {
 #pragma unroll
     for (int j = 0; j < STAGES; ++j)
-      if (g0 + j < total) step(bufp(j), bufp((j + STAGES - 1) % STAGES), g0 + j);
+      if (g0 + j < total) step(bufp(j), bufp((j + STAGES - 1) % STAGES), g0 + j, j);
   }
-  mma_slab(f1);
-  epilogue(n_mine - 1);
+  if constexpr (kDB) {
+    // Last slab of the stream: q = total * SPS - 1.
+    if (SPS == 2 || ((total - 1) & 1)) mma_slab(fr[kDB ? 1 : 0]);
+    else mma_slab(fr[0]);
+    epilogue(n_mine - 1);
+  }
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
 // ---------------------------------------------------------------------------
-// Tile table.  Entries are (BM, BN, waves along M, waves along N); the LDS use
-// is 2 * (BM + BN) * 128 bytes (register-staged kernel, ids 0-4) or
-// 3 * (BM + BN) * 128 bytes (direct-to-LDS kernel, ids 5+, bf16, K % 64 == 0).
+// Tile tables.
 
 struct TileCfg {
   int bm, bn, wgm, wgn;
 };
 
 // bf16 configurations (index = tile id for CGPT_BF16).
+//   ids 0-4: register-staged double buffer (any K % 8), LDS 2*(BM+BN)*128 B
+//   ids 5+ : direct-to-LDS pipeline, persistent (K % (32*SPS) == 0),
+//            LDS STAGES*(BM+BN)*64*SPS B + 1088 B per wave
 static const TileCfg kBf16Tiles[] = {
-    {256, 256, 2, 2},  // 0: 128x128 per wave, 128 KiB LDS
-    {256, 128, 2, 2},  // 1: 128x64 per wave, 96 KiB LDS
-    {128, 128, 2, 2},  // 2: 64x64 per wave, 64 KiB LDS
-    {128, 64, 2, 2},   // 3: 64x32 per wave, 48 KiB LDS
-    {64, 64, 2, 2},    // 4: 32x32 per wave, 32 KiB LDS
-    // direct-to-LDS, 3 stages (K % 64 == 0):
-    {256, 128, 2, 2},  // 5: 4 waves, 128x64 per wave, 144 KiB LDS
-    {256, 128, 4, 2},  // 6: 8 waves, 64x64 per wave, 144 KiB LDS
-    {128, 256, 2, 4},  // 7: 8 waves, 64x64 per wave, 144 KiB LDS
-    {128, 128, 2, 2},  // 8: 4 waves, 64x64 per wave, 96 KiB LDS
-    // direct-to-LDS, 2 stages:
-    {256, 256, 2, 4},  // 9: 8 waves, 128x64 per wave, 128 KiB LDS
-    {256, 256, 2, 2},  // 10: 4 waves, 128x128 per wave, 128 KiB LDS
-    // persistent (one block per CU), direct-to-LDS, K % 64 == 0, K >= 128:
-    {256, 128, 4, 2},  // 11: 8 waves, 64x64 per wave, 3 stages, 144 KiB LDS
-    {128, 256, 2, 4},  // 12: 8 waves, 64x64 per wave, 3 stages, 144 KiB LDS
+    {256, 256, 2, 2},  // 0
+    {256, 128, 2, 2},  // 1
+    {128, 128, 2, 2},  // 2
+    {128, 64, 2, 2},   // 3
+    {64, 64, 2, 2},    // 4
+    {256, 256, 2, 4},  // 5: 8 waves (128x64), SPS 2, 2 stages, 128 KiB
+    {256, 256, 2, 4},  // 6: 8 waves (128x64), SPS 1, 4 stages, 128 KiB
+    {256, 192, 2, 4},  // 7: 8 waves (128x48), SPS 2, 2 stages, 112 KiB
+    {256, 192, 4, 2},  // 8: 8 waves (64x96),  SPS 2, 2 stages, 112 KiB
+    {256, 128, 4, 2},  // 9: 8 waves (64x64),  SPS 2, 3 stages, 144 KiB
+    {128, 256, 2, 4},  // 10: 8 waves (64x64), SPS 2, 3 stages, 144 KiB
+    {256, 128, 4, 2},  // 11: 8 waves (64x64), SPS 1, 6 stages, 144 KiB
 };
-constexpr int kFirstDmaTile = 5;
-constexpr int kFirstPersistTile = 11;
+constexpr int kFirstPipeTile = 5;
+static const int kPipeSps[] = {2, 1, 2, 2, 2, 2, 1};
 // fp32 configurations (index = tile id for CGPT_F32).
 static const TileCfg kF32Tiles[] = {
     {128, 128, 2, 2},  // 0
@@ -678,22 +592,6 @@ static int launch_cfg(const void* a, const void* w, const void* bias, bool bias_
   return hip_status(hipGetLastError());
 }
 
-template <int BM, int BN, int WGM, int WGN, int STAGES, int EPI, typename TOut>
-static int launch_dma(const void* a, const void* w, const void* bias, bool bias_bf16, void* c,
-                      int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc, bool vec_store,
-                      hipStream_t s) {
-  const int tiles_m = (M + BM - 1) / BM;
-  const int tiles_n = (N + BN - 1) / BN;
-  const int64_t blocks = static_cast<int64_t>(tiles_m) * tiles_n;
-  if (blocks > 0x7fffffff) return CGPT_ESHAPE;
-  static_assert(STAGES * (BM + BN) * 128 <= 160 * 1024, "LDS budget of one CU");
-  hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, WGM, WGN, STAGES, EPI, TOut>),
-                     dim3(static_cast<unsigned>(blocks)), dim3(64 * WGM * WGN), 0, s,
-                     static_cast<const bf16_t*>(a), static_cast<const bf16_t*>(w), bias, bias_bf16,
-                     static_cast<TOut*>(c), M, N, K, lda, ldw, ldc, tiles_m, tiles_n, vec_store);
-  return hip_status(hipGetLastError());
-}
-
 // Compute units of the current device (persistent grids launch one block per
 // CU).  Cached per device id; concurrent first calls store the same value.
 static int num_cus() {
@@ -709,27 +607,29 @@ static int num_cus() {
   return cache[dev];
 }
 
-template <int BM, int BN, int WGM, int WGN, int STAGES, int EPI, typename TOut>
-static int launch_persist(const void* a, const void* w, const void* bias, bool bias_bf16, void* c,
-                          int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc,
-                          bool vec_store, hipStream_t s) {
-  static_assert(STAGES * (BM + BN) * 128 <= 160 * 1024, "LDS budget of one CU");
+template <int BM, int BN, int WGM, int WGN, int SPS, int STAGES, int EPI, typename TOut>
+static int launch_pipe(const void* a, const void* w, const void* bias, bool bias_bf16, void* c,
+                       int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc, bool vec_store,
+                       hipStream_t s) {
+  static_assert(STAGES * (BM + BN) * 64 * SPS + (WGM * WGN) * kScrFloats * 4 <= 160 * 1024,
+                "LDS budget of one CU");
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = (N + BN - 1) / BN;
   const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
   if (tiles > 0x7fffffff) return CGPT_ESHAPE;
   const int grid = static_cast<int>(tiles < num_cus() ? tiles : num_cus());
-  hipLaunchKernelGGL((gemm_persist_kernel<BM, BN, WGM, WGN, STAGES, EPI, TOut>), dim3(grid),
+  hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut>), dim3(grid),
                      dim3(64 * WGM * WGN), 0, s, static_cast<const bf16_t*>(a),
                      static_cast<const bf16_t*>(w), bias, bias_bf16, static_cast<TOut*>(c), M, N,
                      K, lda, ldw, ldc, tiles_m, tiles_n, vec_store);
   return hip_status(hipGetLastError());
 }
 
-// The direct-to-LDS kernel addresses A and W through 32-bit buffer offsets and
-// consumes K in steps of 64.
-static bool dma_ok(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) {
-  return K % 64 == 0 && M * lda * 2 < 0x7fffffff && N * ldw * 2 < 0x7fffffff;
+// The pipelined kernel addresses A and W through 32-bit buffer offsets and
+// consumes K in whole stages.
+static bool pipe_ok(int tile, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) {
+  const int sps = kPipeSps[tile - kFirstPipeTile];
+  return K % (32 * sps) == 0 && M * lda * 2 < 0x7fffffff && N * ldw * 2 < 0x7fffffff;
 }
 
 template <typename TIn, int EPI, typename TOut>
@@ -740,6 +640,10 @@ static int launch_tile(int tile, const void* a, const void* w, const void* bias,
   case id:                                                                                    \
     return launch_cfg<TIn, BM, BN, WGM, WGN, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda, \
                                                         ldw, ldc, vec_store, s);
+#define CGPT_PIPE_CASE(id, BM, BN, WGM, WGN, SPS, ST)                                          \
+  case id:                                                                                     \
+    return launch_pipe<BM, BN, WGM, WGN, SPS, ST, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, \
+                                                             lda, ldw, ldc, vec_store, s);
   if constexpr (sizeof(TIn) == 2) {
     switch (tile) {
       CGPT_GEMM_CASE(0, 256, 256, 2, 2)
@@ -747,24 +651,13 @@ static int launch_tile(int tile, const void* a, const void* w, const void* bias,
       CGPT_GEMM_CASE(2, 128, 128, 2, 2)
       CGPT_GEMM_CASE(3, 128, 64, 2, 2)
       CGPT_GEMM_CASE(4, 64, 64, 2, 2)
-#define CGPT_DMA_CASE(id, BM, BN, WGM, WGN, ST)                                                \
-  case id:                                                                                     \
-    return launch_dma<BM, BN, WGM, WGN, ST, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda, \
-                                                       ldw, ldc, vec_store, s);
-      CGPT_DMA_CASE(5, 256, 128, 2, 2, 3)
-      CGPT_DMA_CASE(6, 256, 128, 4, 2, 3)
-      CGPT_DMA_CASE(7, 128, 256, 2, 4, 3)
-      CGPT_DMA_CASE(8, 128, 128, 2, 2, 3)
-      CGPT_DMA_CASE(9, 256, 256, 2, 4, 2)
-      CGPT_DMA_CASE(10, 256, 256, 2, 2, 2)
-#undef CGPT_DMA_CASE
-#define CGPT_PERSIST_CASE(id, BM, BN, WGM, WGN, ST)                                             \
-  case id:                                                                                     \
-    return launch_persist<BM, BN, WGM, WGN, ST, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K,  \
-                                                           lda, ldw, ldc, vec_store, s);
-      CGPT_PERSIST_CASE(11, 256, 128, 4, 2, 3)
-      CGPT_PERSIST_CASE(12, 128, 256, 2, 4, 3)
-#undef CGPT_PERSIST_CASE
+      CGPT_PIPE_CASE(5, 256, 256, 2, 4, 2, 2)
+      CGPT_PIPE_CASE(6, 256, 256, 2, 4, 1, 4)
+      CGPT_PIPE_CASE(7, 256, 192, 2, 4, 2, 2)
+      CGPT_PIPE_CASE(8, 256, 192, 4, 2, 2, 2)
+      CGPT_PIPE_CASE(9, 256, 128, 4, 2, 2, 3)
+      CGPT_PIPE_CASE(10, 128, 256, 2, 4, 2, 3)
+      CGPT_PIPE_CASE(11, 256, 128, 4, 2, 1, 6)
       default: return CGPT_EINVAL;
     }
   } else {
@@ -774,18 +667,18 @@ static int launch_tile(int tile, const void* a, const void* w, const void* bias,
       default: return CGPT_EINVAL;
     }
   }
+#undef CGPT_PIPE_CASE
 #undef CGPT_GEMM_CASE
 }
 
-// Default tile choice (measured on MI355X): tiles of at most 128x128 run 2-3
-// blocks per CU, which hides global-load latency better than one 256-row
-// block; 128x128 wins for long K, 128x64 otherwise, and small grids (fewer
-// than two blocks per CU) drop to the smallest tile.
+// Default tile choice when the caller's table has no entry: the register-staged
+// kernel with the largest tile that still gives every CU about two blocks
+// (128x128 for long K, 128x64 otherwise), smaller tiles for small grids.
 static int auto_tile(bool bf16, int M, int N, int K) {
   const TileCfg* t = bf16 ? kBf16Tiles : kF32Tiles;
   const int nt = bf16 ? kNumBf16Tiles : kNumF32Tiles;
   const int first = bf16 ? (K >= 2048 ? 2 : 3) : 0;
-  const int last = bf16 ? kFirstDmaTile - 1 : nt - 1;
+  const int last = bf16 ? kFirstPipeTile - 1 : nt - 1;
   for (int i = first; i <= last; ++i) {
     const int64_t blocks =
         static_cast<int64_t>((M + t[i].bm - 1) / t[i].bm) * ((N + t[i].bn - 1) / t[i].bn);
@@ -840,8 +733,7 @@ extern "C" int cgpt_gemm(const void* a, const void* w, const void* bias, void* c
   if (tile == CGPT_TILE_AUTO)
     tile = auto_tile(bf16, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K));
   if (tile < 0 || tile >= nt) return CGPT_EINVAL;
-  if (bf16 && tile >= kFirstDmaTile && !dma_ok(M, N, K, lda, ldw)) return CGPT_ESHAPE;
-  if (bf16 && tile >= kFirstPersistTile && K < 128) return CGPT_ESHAPE;
+  if (bf16 && tile >= kFirstPipeTile && !pipe_ok(tile, M, N, K, lda, ldw)) return CGPT_ESHAPE;
   const int64_t out_align = out_dtype == CGPT_F32 ? 16 : 8;
   const bool vec_store = (ldc % 4 == 0) && (reinterpret_cast<uintptr_t>(c) % out_align == 0);
   const bool bias_bf16 = bias_dtype == CGPT_BF16;

@@ -7,15 +7,14 @@ fp16) and the unwired ``TileConfig`` (``cutile_gpt/api/config.py:36-64``).
 Tile ids index the configuration table compiled into libcgpt.so
 (``csrc/gemm.hip``):
 
-    bf16, register-staged double buffer:
+    bf16, register-staged double buffer (any K % 8):
           0 = 256x256 (4 waves, 128x128 each), 1 = 256x128, 2 = 128x128,
           3 = 128x64, 4 = 64x64
-    bf16, direct-to-LDS pipeline (K % 64 == 0):
-          5 = 256x128 (4 waves), 6 = 256x128 (8 waves), 7 = 128x256 (8 waves),
-          8 = 128x128 (4 waves), all 3 stages; 9 = 256x256 (8 waves, 128x64
-          each), 10 = 256x256 (4 waves), 2 stages
-    bf16, persistent direct-to-LDS (one block per CU, K % 64 == 0, K >= 128):
-          11 = 256x128 (8 waves), 12 = 128x256 (8 waves), 3 stages
+    bf16, persistent direct-to-LDS pipeline, 8 waves (K % (32 * slabs) == 0):
+          5 = 256x256, 2 stages of 2 k32 slabs     6 = 256x256, 4 stages of 1
+          7 = 256x192, 2 stages of 2 (128x48/wave) 8 = 256x192 (64x96/wave), 2 of 2
+          9 = 256x128, 3 stages of 2               10 = 128x256, 3 stages of 2
+          11 = 256x128, 6 stages of 1
     fp32: 0 = 128x128, 1 = 64x64
 
 ``TABLE`` maps exact (dtype, M, N, K) problems measured on MI355X to the tile
@@ -34,16 +33,16 @@ from . import _lib
 _B = _lib.CGPT_BF16
 TABLE: Dict[Tuple[int, int, int, int], int] = {
     # GPT-2 124M prefill, M = 16 x 1024
-    (_B, 16384, 2304, 768): 11,   # c_attn      594
-    (_B, 16384, 768, 768): 12,    # attn c_proj 493
-    (_B, 16384, 3072, 768): 12,   # c_fc        651
-    (_B, 16384, 768, 3072): 9,    # mlp c_proj  828
-    (_B, 16384, 50257, 768): 9,   # lm head     646 (fp32 logits)
+    (_B, 16384, 2304, 768): 7,    # c_attn       754
+    (_B, 16384, 768, 768): 7,     # attn c_proj  684
+    (_B, 16384, 3072, 768): 5,    # c_fc         795
+    (_B, 16384, 768, 3072): 7,    # mlp c_proj  1044
+    (_B, 16384, 50257, 768): 5,   # lm head      665 (bf16 out)
     # 'medium' (8L, d 512) prefill, M = 16 x 256
-    (_B, 4096, 1536, 512): 11,    # 358
-    (_B, 4096, 2048, 512): 11,    # 451
+    (_B, 4096, 1536, 512): 10,    # 375
+    (_B, 4096, 2048, 512): 9,     # 474
     (_B, 4096, 512, 2048): 3,     # 271
-    (_B, 4096, 50257, 512): 12,   # 376
+    (_B, 4096, 50257, 512): 5,    # 512
 }
 
 

@@ -131,7 +131,7 @@ def test_gemm_every_bf16_tile(gpu, tile, m, n, k):
     close(out, gemm_ref(a, w, b, _lib.EPI_BIAS), 1e-3, 2 ** -8, f"tile {tile}")
 
 
-DMA_TILES = [5, 6, 7, 8, 9, 10]
+DMA_TILES = [5, 6, 7, 8, 9, 10, 11]
 
 
 @pytest.mark.parametrize("tile", DMA_TILES)
@@ -148,7 +148,7 @@ def test_gemm_dma_tiles(gpu, tile, m, n, k, epi):
     close(out, ref, 1e-4 * math.sqrt(k / 64), 1e-5, f"dma tile {tile} {m}x{n}x{k}")
 
 
-PERSIST_TILES = [11, 12]
+PERSIST_TILES = [5, 7, 9, 10, 11]
 
 
 @pytest.mark.parametrize("tile", PERSIST_TILES)
@@ -166,17 +166,17 @@ def test_gemm_persistent_tiles(gpu, tile, m, n, k, epi):
     close(out, ref, 2e-3, 2 ** -8, f"persistent tile {tile} {m}x{n}x{k}")
 
 
-def test_gemm_persistent_rejects_single_k_step(gpu):
-    a = randn(64, 64, dtype=BF16).to(gpu)
-    with pytest.raises(ValueError):
-        cg.kernels._gemm(a, a, None, _lib.EPI_NONE, F32, "t", tile=11)
-
-
-def test_gemm_dma_rejects_ragged_k(gpu):
+def test_gemm_pipe_rejects_ragged_k(gpu):
     a = randn(64, 72, dtype=BF16).to(gpu)
     w = randn(64, 72, dtype=BF16).to(gpu)
     with pytest.raises(ValueError):
         cg.kernels._gemm(a, w, None, _lib.EPI_NONE, F32, "t", tile=5)
+    a = randn(64, 96, dtype=BF16).to(gpu)  # K % 64 != 0 but K % 32 == 0: only SPS 1 tiles
+    w = randn(64, 96, dtype=BF16).to(gpu)
+    with pytest.raises(ValueError):
+        cg.kernels._gemm(a, w, None, _lib.EPI_NONE, F32, "t", tile=5)
+    out = cg.kernels._gemm(a, w, None, _lib.EPI_NONE, F32, "t", tile=6)
+    close(out, gemm_ref(a.cpu(), w.cpu(), None, 0), 1e-3, 1e-4, "K=96 on a single-slab tile")
 
 
 @pytest.mark.parametrize("tile", range(2))
