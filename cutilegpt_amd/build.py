@@ -36,8 +36,17 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the cutilegpt_amd kernels need ROCm's hipcc")
 
 
+# Per-file flags.  Attention rescales and exponentiates its MFMA accumulators
+# in the VALU every KV block; the VGPR form of the MFMAs keeps them out of the
+# AGPRs (no v_accvgpr_read/write shuttling).
+FILE_FLAGS = {
+    "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: str, obj: str, extra) -> None:
-    cmd = [hipcc(), *HIPCC_FLAGS, *extra, "-c", src, "-o", obj]
+    cmd = [hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), *extra,
+           "-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {os.path.basename(src)}:\n{res.stderr}")

@@ -83,7 +83,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
   static_assert(HD % 16 == 0, "head_dim must be a multiple of 16");
   __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // readfirstlane: the wave index is uniform, so wave-level conditions below
+  // become scalar branches instead of exec-masked code.
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, frow = lane & 15;
 
   const int n_qblk = (Tq + BQ - 1) / BQ;
@@ -219,7 +221,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
           for (int qt = 0; qt < QT; ++qt) AttnMfma<T>::run(kf, qf[qt][ks], s[qt][kt]);
         }
       }
-      // Online softmax (base 2).  Masking only where the block can be partial.
+      // Online softmax (base 2) on raw scores: p = exp2(s * scale_log2 - m) is
+      // one FMA feeding v_exp_f32.  The shift m of a row only moves when the
+      // row's block maximum exceeds it by more than kLazyLog2 (so P <= 2^8):
+      // softmax is invariant to the shift, and the rescale of O and l (which
+      // pulls the accumulators through the VALU) then runs only on the few
+      // blocks where some row's maximum jumps, instead of on every block.
+      // Masking is branch-free and only on blocks that straddle the diagonal
+      // or the end of the sequence.
+      constexpr float kLazyLog2 = 8.0f;
       const bool need_mask = (causal && kv0 + BKV - 1 > wave_q0 + off) || (kv0 + BKV > Tk);
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) {
@@ -229,34 +239,40 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            float x = s[qt][kt][r] * scale_log2;
+            float x = s[qt][kt][r];
             if (need_mask) {
               const int key = kv0 + kt * 16 + 4 * g + r;
-              if (key >= Tk || (causal && key > qpos)) x = -INFINITY;
+              x = (key >= Tk || (causal && key > qpos)) ? -INFINITY : x;
+              s[qt][kt][r] = x;
             }
-            s[qt][kt][r] = x;
             mloc = fmaxf(mloc, x);
           }
         mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-        const float m_new = fmaxf(m_run[qt], mloc);
-        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m_run[qt] - m_use);
-        m_run[qt] = m_new;
+        const float mblk = mloc * scale_log2;  // scale > 0: max commutes
+        const bool grow = mblk > m_run[qt] + kLazyLog2;
+        if (__any(grow)) {
+          const float m_new = grow ? mblk : m_run[qt];
+          const float alpha = grow ? __builtin_amdgcn_exp2f(m_run[qt] - m_new) : 1.0f;
+          m_run[qt] = m_new;
+          l_run[qt] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o_acc[qt][dt][r] *= alpha;
+        }
+        // A row that has seen only masked keys keeps m = -inf; its p are 0.
+        const float neg_m = m_run[qt] == -INFINITY ? 0.f : -m_run[qt];
         float lsum = 0.f;
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float p = __builtin_amdgcn_exp2f(s[qt][kt][r] - m_use);
+            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qt][kt][r], scale_log2, neg_m));
             s[qt][kt][r] = p;
             lsum += p;
           }
-        l_run[qt] = l_run[qt] * alpha + lsum;
-#pragma unroll
-        for (int dt = 0; dt < ND; ++dt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) o_acc[qt][dt][r] *= alpha;
+        l_run[qt] += lsum;
       }
       // O^T += V^T P^T
       if constexpr (sizeof(T) == 2) {

@@ -121,7 +121,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm0 = (wave / WGN) * WM;
   const int wn0 = (wave % WGN) * WN;
 
@@ -328,7 +328,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
   __shared__ __attribute__((aligned(1024))) uint8_t st5[STAGES > 5 ? STAGE : 16];
   __shared__ float escr[NW][kScrFloats];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
   const int frow = lane & 15, fgrp = lane >> 4;
   const int lrow = lane / CPR, pchunk = lane % CPR;
