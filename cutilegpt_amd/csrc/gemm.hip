@@ -54,6 +54,23 @@ __device__ __forceinline__ void store4_out(bf16_t* p, const float* v) {
   *reinterpret_cast<u32x2_t*>(p) = u;
 }
 
+#if defined(__HIP_DEVICE_COMPILE__)
+// Four consecutive outputs through a buffer resource: a store whose byte
+// offset lies at or past the resource's size is dropped by the hardware, so
+// callers pass an out-of-range offset instead of branching around the store.
+__device__ __forceinline__ void buffer_store4(__amdgpu_buffer_rsrc_t r, uint32_t off, const float* v,
+                                              float*) {
+  __builtin_amdgcn_raw_buffer_store_b128(
+      u32x4_t{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])},
+      r, off, 0, 0);
+}
+__device__ __forceinline__ void buffer_store4(__amdgpu_buffer_rsrc_t r, uint32_t off, const float* v,
+                                              bf16_t*) {
+  __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])}, r,
+                                        off, 0, 0);
+}
+#endif
+
 __device__ __forceinline__ float load_bias(const void* bias, bool bf16, int64_t n) {
   return bf16 ? bf16_to_f32(static_cast<const bf16_t*>(bias)[n]) : static_cast<const float*>(bias)[n];
 }
@@ -73,6 +90,8 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
   tm = first_m + in_group % gsz;
   tn = in_group / gsz;
 }
+
+
 
 // Per-wave LDS scratch for re-mapping one 16x16 output block (17-float rows:
 // conflict-free column and row accesses).
@@ -250,25 +269,48 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(
 //   within a tile; the K advance is the scalar offset.  Rows past M (or N) are
 //   clamped to the last row, so every access stays inside the matrix.
 // * A stage holds SPS k32 slabs (LDS rows of 64 * SPS bytes); STAGES stages
-//   rotate through distinct __shared__ arrays.  Stage g + STAGES - 1 is issued
-//   right after the barrier of step g; before that barrier each wave waits
-//   (s_waitcnt vmcnt) until only its own later stages are still in flight, then
-//   a raw s_barrier publishes every wave's part.  A full __syncthreads would
-//   add a release fence, i.e. vmcnt(0), and collapse the pipeline to one stage;
-//   the empty asm statements keep the compiler from moving LDS accesses across
-//   the barrier, and lgkmcnt(0) in the same wait retires the previous stage's
-//   LDS reads before its buffer is refilled.
-// * Fragment reads are software-pipelined: the slab read after a barrier
-//   overlaps the MFMAs of the previous slab (held in the other fragment set).
+//   rotate through distinct __shared__ arrays.  Step g: raw s_barrier (every
+//   wave has already waited for its own part of stage g), issue stage
+//   g + STAGES - 1 into the buffer freed by step g - 1, read + MFMA the SPS
+//   slabs of stage g, then wait (s_waitcnt vmcnt) until stage g + 1 has
+//   landed, leaving only later stages (and the epilogue's stores, below) in
+//   flight.  A full __syncthreads would add a release fence, i.e. vmcnt(0),
+//   and collapse the pipeline to one stage; the empty asm statements keep the
+//   compiler from moving LDS accesses across the barrier, and lgkmcnt(0) in
+//   the same wait retires this step's LDS reads before the buffer is refilled.
 // * Persistent: block b walks tiles b, b + grid, ...; their K stages form one
 //   flattened stream, so the first stages of tile i+1 are in flight while tile
-//   i finishes.  A tile's bias is fetched right after the barrier of its last
-//   step (before that step's DMA), so the epilogue one step later finds it in
-//   registers without draining the DMA queue; the step after an epilogue waits
-//   for every outstanding transfer (its stores count in vmcnt too).
+//   i finishes.  The bias of the current tile is reloaded at every step before
+//   the DMA (so it is older than anything a wait counts); the epilogue ends a
+//   tile's last step.  With buffer-resource stores an epilogue issues exactly
+//   TM * TN stores per wave and the following wait leaves them in flight;
+//   otherwise that wait drains everything.
 // Requires K % (32 * SPS) == 0.
 
 #define CGPT_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
+#if defined(__HIP_DEVICE_COMPILE__)
+// Raw buffer descriptor (base, no stride, `bytes` records, gfx9 raw format).
+__device__ __forceinline__ u32x4_t buffer_desc(const void* p, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  return u32x4_t{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32) & 0xffffu, bytes,
+                 0x00020000u};
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint8_t*)(p)));
+}
+// Global -> LDS DMA of 16 bytes per lane: lane l's bytes land at M0 + 16 l.  Issued from inline assembly on purpose: the compiler then
+// neither counts these loads nor guards later LDS reads against them, so the
+// stage pipeline's own vmcnt waits and barriers are the only synchronisation
+// (the compiler cannot prove that a read of one stage buffer does not alias
+// the DMA into another and would otherwise drain the queue before every
+// read).  M0 needs one wait state after its write.
+__device__ __forceinline__ void dma_lds16(u32x4_t desc, uint32_t lds, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(lds), "v"(voff), "s"(desc), "s"(soff) : "memory", "m0");
+}
+#endif
 
 __device__ __forceinline__ void raw_barrier() {
   asm volatile("" ::: "memory");
@@ -284,20 +326,34 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
 }
 
-// Wait until at most `later` stages of LPS loads each are in flight.
-template <int LPS, int MAXLATER>
-__device__ __forceinline__ void wait_stages(int later) {
+// Wait until the stage that has `later` stages of LPS loads each issued after
+// it, plus (when `stores`) ST stores, has landed: vmcnt retires loads and
+// stores in issue order.
+template <int LPS, int MAXLATER, int ST>
+__device__ __forceinline__ void wait_stages(int later, bool stores) {
   static_assert(MAXLATER <= 4, "up to 6 stages");
-  if (MAXLATER >= 4 && later >= 4) { wait_vmcnt<4 * LPS>(); return; }
-  if (MAXLATER >= 3 && later >= 3) { wait_vmcnt<3 * LPS>(); return; }
-  if (MAXLATER >= 2 && later >= 2) { wait_vmcnt<2 * LPS>(); return; }
-  if (MAXLATER >= 1 && later >= 1) { wait_vmcnt<1 * LPS>(); return; }
+  static_assert(MAXLATER * LPS + ST < 64, "vmcnt range");
+  if (stores) {
+    if constexpr (MAXLATER >= 4) if (later >= 4) { wait_vmcnt<4 * LPS + ST>(); return; }
+    if constexpr (MAXLATER >= 3) if (later >= 3) { wait_vmcnt<3 * LPS + ST>(); return; }
+    if constexpr (MAXLATER >= 2) if (later >= 2) { wait_vmcnt<2 * LPS + ST>(); return; }
+    if constexpr (MAXLATER >= 1) if (later >= 1) { wait_vmcnt<1 * LPS + ST>(); return; }
+    wait_vmcnt<ST>();
+    return;
+  }
+  if constexpr (MAXLATER >= 4) if (later >= 4) { wait_vmcnt<4 * LPS>(); return; }
+  if constexpr (MAXLATER >= 3) if (later >= 3) { wait_vmcnt<3 * LPS>(); return; }
+  if constexpr (MAXLATER >= 2) if (later >= 2) { wait_vmcnt<2 * LPS>(); return; }
+  if constexpr (MAXLATER >= 1) if (later >= 1) { wait_vmcnt<1 * LPS>(); return; }
   wait_vmcnt<0>();
 }
 
 constexpr uint32_t kBufferRsrcWord3 = 0x00020000u;  // raw buffer, gfx9 family
 
-template <int BM, int BN, int WGM, int WGN, int SPS, int STAGES, int EPI, typename TOut>
+
+// BUFST: every output store goes through a buffer resource (requires N % 4 == 0
+// and 16/8-byte aligned rows); otherwise plain stores behind per-lane bounds.
+template <int BM, int BN, int WGM, int WGN, int SPS, int STAGES, int EPI, typename TOut, bool BUFST>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
     const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, const void* __restrict__ bias,
     bool bias_bf16, TOut* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldw,
@@ -319,7 +375,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
   static_assert(STAGES >= 2 && STAGES <= 6, "2..6 stages");
   static_assert(SPS == 2 || STAGES % 2 == 0, "single-slab stages alternate fragment sets");
   static_assert(BM % (RPI * NW) == 0 && BN % (RPI * NW) == 0, "tile/wave mismatch");
-  static_assert((STAGES - 2) * LPS < 64, "vmcnt range");
+  static_assert((STAGES - 2) * LPS + TM * TN < 64, "vmcnt range");
   __shared__ __attribute__((aligned(1024))) uint8_t st0[STAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t st1[STAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t st2[STAGES > 2 ? STAGE : 16];
@@ -334,10 +390,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
   const int lrow = lane / CPR, pchunk = lane % CPR;
   auto swz = [](int row) { return ROWB == 128 ? (row & 7) : ((row >> 1) & 3); };
 
-  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<bf16_t*>(A), 0, static_cast<int>(static_cast<int64_t>(M) * lda * 2), kBufferRsrcWord3);
-  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<bf16_t*>(W), 0, static_cast<int>(static_cast<int64_t>(N) * ldw * 2), kBufferRsrcWord3);
+  const u32x4_t ra = buffer_desc(A, static_cast<uint32_t>(static_cast<int64_t>(M) * lda * 2));
+  const u32x4_t rw = buffer_desc(W, static_cast<uint32_t>(static_cast<int64_t>(N) * ldw * 2));
 
   const int n_tiles = tiles_m * tiles_n;
   const int KT = K / (32 * SPS);
@@ -369,12 +423,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
     const int soff = iss_kt * ROWB;
 #pragma unroll
     for (int ii = 0; ii < A_INS; ++ii)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, CGPT_LDS(buf + (ii * NW + wave) * 1024), 16,
-                                               aoff[ii], soff, 0, 0);
+      dma_lds16(ra, lds_addr(buf + (ii * NW + wave) * 1024), aoff[ii], soff);
 #pragma unroll
     for (int ii = 0; ii < W_INS; ++ii)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, CGPT_LDS(buf + BM * ROWB + (ii * NW + wave) * 1024),
-                                               16, woff[ii], soff, 0, 0);
+      dma_lds16(rw, lds_addr(buf + BM * ROWB + (ii * NW + wave) * 1024), woff[ii], soff);
     if (++iss_kt == KT) {
       iss_kt = 0;
       if (++iss_i < n_mine) set_offsets(iss_i);
@@ -412,23 +464,91 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
       for (int j = 0; j < TN; ++j) Mfma<bf16_t>::run(f.w[j], f.a[i], acc[i][j]);
   };
 
-  f32x4_t bval[TN];
-  auto load_bias_tile = [&](int i) {
+  // Bias of the tile being computed, reloaded at every step (before the
+  // step's DMA, so the loads are older than everything a wait counts) and
+  // used by the epilogue at the tile's last step.  With buffer stores N % 4 ==
+  // 0, so each 4-column group is one aligned vector load with no branch on the
+  // bias type (groups past N read the last group); otherwise each element's
+  // dword is loaded, clamped into [0, N): byte (n+r)*4 (fp32) or
+  // ((n+r)*2) & ~3 (bf16, half by parity).
+  uint32_t braw[TN][4];
+  int cmp_n0;
+  {
     int tm, tn;
-    tile_coords(static_cast<int>(blockIdx.x) + i * static_cast<int>(gridDim.x), tiles_m, tiles_n,
-                tm, tn);
+    tile_coords(static_cast<int>(blockIdx.x), tiles_m, tiles_n, tm, tn);
+    cmp_n0 = tn * BN;
+  }
+  const int bshift = bias_bf16 ? 1 : 2;
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(bias), 0, EPI != CGPT_EPI_NONE ? N << bshift : 0, kBufferRsrcWord3);
+  auto load_bias = [&]() {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const int n = tn * BN + wn0 + j * 16 + 4 * fgrp;
+      const int n = cmp_n0 + wn0 + j * 16 + 4 * fgrp;
+      if constexpr (BUFST) {
+        // 16 bytes from the group's first element whatever the type (bf16
+        // uses the first 8); bytes past the bias read as zero.
+        const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rb, min(n, N - 4) << bshift, 0, 0);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) bval[j][r] = n + r < N ? load_bias(bias, bias_bf16, n + r) : 0.f;
+        for (int r = 0; r < 4; ++r) braw[j][r] = v[r];
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int idx = min(n + r, N - 1);
+          braw[j][r] = *reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(bias) +
+                                                          ((idx << bshift) & ~3));
+        }
+      }
     }
   };
-  auto epilogue = [&](int i) {
+  auto bias_at = [&](int j, int r, int n) -> float {
+    if constexpr (BUFST) {
+      if (!bias_bf16) return __uint_as_float(braw[j][r]);
+      const uint32_t w = braw[j][r >> 1];
+      return __uint_as_float((r & 1) ? (w & 0xffff0000u) : (w << 16));
+    } else {
+      const uint32_t w = braw[j][r];
+      if (!bias_bf16) return __uint_as_float(w);
+      return __uint_as_float((min(n + r, N - 1) & 1) ? (w & 0xffff0000u) : (w << 16));
+    }
+  };
+  // Returns true when the tile took the buffer-store path, which issues exactly
+  // TM * TN stores per wave (rows past M lie past the resource's size and
+  // columns past N get an offset past it, so both are dropped), and the next
+  // wait can leave them in flight.  Plain stores sit behind per-lane
+  // conditions, so the next wait drains everything.
+  auto epilogue = [&](int i) -> bool {
     int tm, tn;
     tile_coords(static_cast<int>(blockIdx.x) + i * static_cast<int>(gridDim.x), tiles_m, tiles_n,
                 tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
+    if constexpr (BUFST) {
+      const int rows = min(BM, M - m0);
+      const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+          C + static_cast<int64_t>(m0) * ldc, 0,
+          static_cast<int>(static_cast<int64_t>(rows) * ldc * static_cast<int64_t>(sizeof(TOut))),
+          kBufferRsrcWord3);
+#pragma unroll
+      for (int ii = 0; ii < TM; ++ii) {
+        const uint32_t roff = static_cast<uint32_t>((wm0 + ii * 16 + frow) * ldc);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int n = n0 + wn0 + j * 16 + 4 * fgrp;
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float t = acc[ii][j][r];
+            if (EPI != CGPT_EPI_NONE) t += bias_at(j, r, n);
+            if (EPI == CGPT_EPI_BIAS_GELU) t = gelu_tanh(t);
+            v[r] = t;
+          }
+          const uint32_t off =
+              n < N ? (roff + static_cast<uint32_t>(n)) * static_cast<uint32_t>(sizeof(TOut)) : 0x80000000u;
+          buffer_store4(rc, off, v, static_cast<TOut*>(nullptr));
+        }
+      }
+      return true;
+    }
 #pragma unroll
     for (int ii = 0; ii < TM; ++ii) {
       const int mb = m0 + wm0 + ii * 16;
@@ -441,7 +561,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           float t = acc[ii][j][r];
-          if (EPI != CGPT_EPI_NONE) t += bval[j][r];
+          if (EPI != CGPT_EPI_NONE) t += bias_at(j, r, n);
           if (EPI == CGPT_EPI_BIAS_GELU) t = gelu_tanh(t);
           v[r] = t;
         }
@@ -459,64 +579,53 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
         }
       }
     }
+    return false;
   };
 
-  // With one wave per SIMD (4-wave blocks) fragment reads are double-buffered
-  // across slabs so a wave overlaps its own LDS reads with its MFMAs; with two
-  // waves per SIMD the other wave covers that latency and a single fragment
-  // set keeps the register budget (256 per wave) free of spills.
-  constexpr bool kDB = NW == 4;
-  Frag fr[kDB ? 2 : 1];
+  Frag fr;
   int cmp_i = 0, cmp_kt = 0;
-  bool after_epi = false;
-  // One flattened step g on stage buffer `cur`; `dst` receives stage g+STAGES-1.
-  // Double-buffered: slab q of the stream (q = g*SPS + s) is read into
-  // fr[q % 2] while the MFMAs of slab q-1 run from fr[(q-1) % 2] (with SPS == 1
-  // the parity is j % 2), and a tile's epilogue runs at the next tile's first
-  // step.  Single set: read slab, MFMA slab; the epilogue ends the tile's last
-  // step.
-  auto step = [&](const uint8_t* cur, uint8_t* dst, int g, int j) {
-    int later = total - 1 - g;
+  // Wait until stage `h` has landed: `later` stages issued after it may stay
+  // in flight, and so may the exact TM * TN buffer stores of an epilogue
+  // issued after them.
+  auto wait_for = [&](int h, bool stores) {
+    int later = total - 1 - h;
     later = later < STAGES - 2 ? later : STAGES - 2;
-    if (after_epi) later = 0;
-    wait_stages<LPS, STAGES - 2>(later);
+    // Younger than stage h: `later` stages, and possibly an epilogue's stores.
+    wait_stages<LPS, STAGES - 2, TM * TN>(later, stores);
+  };
+  // One flattened step g on stage buffer `cur`; `dst` receives stage
+  // g + STAGES - 1.  Every wave enters having waited for stage g itself; the
+  // barrier makes all waves' parts of it visible.  The step ends with the
+  // tile's epilogue when it is the tile's last, then waits for stage g + 1 in
+  // the same straight-line code as the stores, so the wait can count them.
+  auto step = [&](const uint8_t* cur, uint8_t* dst, int g) {
     raw_barrier();
-    after_epi = false;
     const bool last = cmp_kt == KT - 1;
-    if (EPI != CGPT_EPI_NONE && last) load_bias_tile(cmp_i);
+    if (EPI != CGPT_EPI_NONE) load_bias();
     if (g + STAGES - 1 < total) issue(dst);
-    if constexpr (kDB) {
 #pragma unroll
-      for (int s = 0; s < SPS; ++s) {
-        const int p = SPS == 2 ? s : (j & 1);
-        Frag& now = fr[p];
-        Frag& prev = fr[p ^ 1];
-        if (s == 0 && cmp_kt == 0 && g > 0) {
-          mma_slab(prev);
-          epilogue(cmp_i - 1);
-          zero_acc();
-          after_epi = true;
-          read_slab(cur, s, now);
-        } else {
-          read_slab(cur, s, now);
-          if (g > 0 || s > 0) mma_slab(prev);
-        }
+    for (int s = 0; s < SPS; ++s) {
+      read_slab(cur, s, fr);
+      mma_slab(fr);
+    }
+    if (last) {
+      if (epilogue(cmp_i)) {
+        zero_acc();
+        wait_for(g + 1, true);
+      } else {
+        zero_acc();
+        wait_vmcnt<0>();
       }
     } else {
-#pragma unroll
-      for (int s = 0; s < SPS; ++s) {
-        read_slab(cur, s, fr[0]);
-        mma_slab(fr[0]);
-      }
-      if (last) {
-        epilogue(cmp_i);
-        zero_acc();
-        after_epi = true;
-      }
+      wait_for(g + 1, false);
     }
     if (++cmp_kt == KT) {
       cmp_kt = 0;
       ++cmp_i;
+      int tm, tn;
+      tile_coords(static_cast<int>(blockIdx.x) + cmp_i * static_cast<int>(gridDim.x), tiles_m, tiles_n,
+                  tm, tn);
+      cmp_n0 = tn * BN;
     }
   };
 
@@ -528,16 +637,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
     if (s < total) issue(bufp(s));
+  wait_for(0, false);
   for (int g0 = 0; g0 < total; g0 += STAGES) {
 #pragma unroll
     for (int j = 0; j < STAGES; ++j)
-      if (g0 + j < total) step(bufp(j), bufp((j + STAGES - 1) % STAGES), g0 + j, j);
-  }
-  if constexpr (kDB) {
-    // Last slab of the stream: q = total * SPS - 1.
-    if (SPS == 2 || ((total - 1) & 1)) mma_slab(fr[kDB ? 1 : 0]);
-    else mma_slab(fr[0]);
-    epilogue(n_mine - 1);
+      if (g0 + j < total) step(bufp(j), bufp((j + STAGES - 1) % STAGES), g0 + j);
   }
 #endif  // __HIP_DEVICE_COMPILE__
 }
@@ -618,10 +722,20 @@ static int launch_pipe(const void* a, const void* w, const void* bias, bool bias
   const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
   if (tiles > 0x7fffffff) return CGPT_ESHAPE;
   const int grid = static_cast<int>(tiles < num_cus() ? tiles : num_cus());
-  hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut>), dim3(grid),
-                     dim3(64 * WGM * WGN), 0, s, static_cast<const bf16_t*>(a),
-                     static_cast<const bf16_t*>(w), bias, bias_bf16, static_cast<TOut*>(c), M, N,
-                     K, lda, ldw, ldc, tiles_m, tiles_n, vec_store);
+  // Buffer-resource stores write whole 4-column groups and address one tile's
+  // rows with 31-bit byte offsets.
+  const bool buf_store = vec_store && N % 4 == 0 &&
+                         static_cast<int64_t>(BM) * ldc * static_cast<int64_t>(sizeof(TOut)) < 0x7fffffff;
+  if (buf_store)
+    hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut, true>), dim3(grid),
+                       dim3(64 * WGM * WGN), 0, s, static_cast<const bf16_t*>(a),
+                       static_cast<const bf16_t*>(w), bias, bias_bf16, static_cast<TOut*>(c), M, N,
+                       K, lda, ldw, ldc, tiles_m, tiles_n, vec_store);
+  else
+    hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut, false>), dim3(grid),
+                       dim3(64 * WGM * WGN), 0, s, static_cast<const bf16_t*>(a),
+                       static_cast<const bf16_t*>(w), bias, bias_bf16, static_cast<TOut*>(c), M, N,
+                       K, lda, ldw, ldc, tiles_m, tiles_n, vec_store);
   return hip_status(hipGetLastError());
 }
 
@@ -729,6 +843,7 @@ extern "C" int cgpt_gemm(const void* a, const void* w, const void* bias, void* c
   if (lda % epc != 0 || ldw % epc != 0) return CGPT_EINVAL;
   if ((reinterpret_cast<uintptr_t>(a) & 15) || (reinterpret_cast<uintptr_t>(w) & 15))
     return CGPT_EINVAL;
+  if (epilogue != CGPT_EPI_NONE && (reinterpret_cast<uintptr_t>(bias) & 15)) return CGPT_EINVAL;
   const int nt = bf16 ? kNumBf16Tiles : kNumF32Tiles;
   if (tile == CGPT_TILE_AUTO)
     tile = auto_tile(bf16, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K));

@@ -148,7 +148,7 @@ def _gemm(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], e
     out_dtype = out_dtype or x.dtype
     if out is None:
         out = torch.empty((m, n), dtype=out_dtype, device=x.device)
-    b = None if bias is None else bias.contiguous()
+    b = None if bias is None else _aligned(bias)
     lib = _lib.load()
     in_code = _dtype_code(a, name)
     t = gemm_tile(in_code, m, n, k) if tile is None else tile

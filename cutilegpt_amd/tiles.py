@@ -33,16 +33,16 @@ from . import _lib
 _B = _lib.CGPT_BF16
 TABLE: Dict[Tuple[int, int, int, int], int] = {
     # GPT-2 124M prefill, M = 16 x 1024
-    (_B, 16384, 2304, 768): 7,    # c_attn       754
-    (_B, 16384, 768, 768): 7,     # attn c_proj  684
-    (_B, 16384, 3072, 768): 5,    # c_fc         795
-    (_B, 16384, 768, 3072): 7,    # mlp c_proj  1044
-    (_B, 16384, 50257, 768): 5,   # lm head      665 (bf16 out)
+    (_B, 16384, 2304, 768): 7,    # c_attn       758
+    (_B, 16384, 768, 768): 7,     # attn c_proj  713
+    (_B, 16384, 3072, 768): 7,    # c_fc         814
+    (_B, 16384, 768, 3072): 7,    # mlp c_proj  1073
+    (_B, 16384, 50257, 768): 5,   # lm head      650 (bf16 out)
     # 'medium' (8L, d 512) prefill, M = 16 x 256
-    (_B, 4096, 1536, 512): 10,    # 375
-    (_B, 4096, 2048, 512): 9,     # 474
+    (_B, 4096, 1536, 512): 10,    # 397
+    (_B, 4096, 2048, 512): 10,    # 515
     (_B, 4096, 512, 2048): 3,     # 271
-    (_B, 4096, 50257, 512): 5,    # 512
+    (_B, 4096, 50257, 512): 5,    # 516
 }
 
 

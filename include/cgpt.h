@@ -81,7 +81,7 @@ int cgpt_add_layernorm(const void* x, const void* delta, void* x_out,
  * in_dtype is the type of A and W (both CGPT_BF16 -> bf16 MFMA, both CGPT_F32 ->
  * fp32 MFMA); accumulation is fp32; bias (bias_dtype) is added in fp32; C is
  * written as out_dtype.  Requires K % 8 == 0 (bf16) or K % 4 == 0 (fp32), lda /
- * ldw multiples of 8 (bf16) or 4 (fp32) elements and 16-byte aligned A and W.
+ * ldw multiples of 8 (bf16) or 4 (fp32) elements and 16-byte aligned A, W and bias.
  * `tile` selects a tile configuration (CGPT_TILE_AUTO = library heuristic).
  * Replaces cutile_linear / cutile_linear_bias, cutile_gpt/kernels/linear.py:112-222
  * (kernels :37-109); CGPT_EPI_BIAS_GELU also absorbs cutile_gelu at
