@@ -24,6 +24,7 @@ EPI_NONE = 0
 EPI_BIAS = 1
 EPI_BIAS_GELU = 2
 TILE_AUTO = -1
+TILE_SKINNY = -2
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -42,6 +43,13 @@ SIGNATURES = {
                                 _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
                                 _I64, _I64, _I64, _F, _I, _I, _P]),
     "cgpt_embedding": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _P, _P]),
+    "cgpt_embedding_at": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _I, _I, _P, _P]),
+    "cgpt_attention_decode": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P,
+                                   _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+                                   _I64, _I64, _F, _I, _P, _P]),
+    "cgpt_kv_store": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+                           _I64, _I64, _I64, _I64, _I64, _I64, _I, _P]),
+    "cgpt_argmax": (_I, [_P, _I64, _I64, _I64, _I, _P, _P, _I64, _P, _P]),
 }
 
 ABI_VERSION = 1

@@ -98,6 +98,35 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
+// One 16x16 MFMA tile step with 16-byte operand fragments: lane l supplies
+// row l % 16 and k chunk l / 16 of each operand.  bf16: one
+// v_mfma_f32_16x16x32_bf16 (8 k per lane).  fp32: four v_mfma_f32_16x16x4_f32;
+// lane group g supplies k = 4g + j to the j-th (a consistent permutation of the
+// k axis leaves the dot product unchanged).  With operand a = 16 rows of W and
+// b = 16 rows of A, lane l of c holds C[m = l % 16][n = 4(l/16) .. +3].
+template <typename T> struct Mfma;
+template <> struct Mfma<bf16_t> {
+  __device__ static void run(const u32x4_t& a, const u32x4_t& b, f32x4_t& c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma<float> {
+  __device__ static void run(const u32x4_t& a, const u32x4_t& b, f32x4_t& c) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[j]), __uint_as_float(b[j]), c, 0,
+                                               0, 0);
+  }
+};
+
+__device__ __forceinline__ void store4_out(float* p, const float* v) { store_vec(p, v); }
+__device__ __forceinline__ void store4_out(bf16_t* p, const float* v) {
+  u32x2_t u = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  *reinterpret_cast<u32x2_t*>(p) = u;
+}
+
+
 // Error codes shared with the C ABI (see include/cgpt.h).
 __host__ __forceinline__ int hip_status(hipError_t e) {
   return e == hipSuccess ? CGPT_OK : static_cast<int>(e);

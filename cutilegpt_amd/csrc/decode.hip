@@ -1,0 +1,436 @@
+// Incremental (KV-cache) decoding kernels: the pieces a greedy generation
+// step needs beyond the prefill kernels.
+//
+//  * gemm_skinny_kernel — C[M,N] = epi(A W^T + bias) for M <= 64 (one row per
+//    sequence in the batch).  Decode GEMMs are weight-streaming: every weight
+//    byte is read once per step, so the kernel is built around HBM traffic,
+//    not MFMA reuse.  Block = 8 waves sharing one 16-column slice of W; each
+//    wave streams a contiguous K range of those 16 rows straight from global
+//    memory into registers in MFMA fragment order (lane l: row l % 16, k chunk
+//    l / 16 — the same 16-byte fragments the prefill GEMM reads from LDS), with
+//    8 slabs of loads in flight, and multiplies them against the (L2-resident)
+//    activation rows.  The 8 partial 16 x M accumulators are summed through
+//    LDS, then bias / GELU / store.  No workspace, deterministic.
+//  * attn_decode_kernel — one block per (batch, head): appends the step's key
+//    and value to the cache at position pos, then softmax(q K^T * scale) V
+//    over cache rows 0..pos.  pos = pos_base + *pos_dev, read on the device so
+//    one captured launch sequence serves every step.
+//  * kv_store_kernel — copies a prefill's keys and values into the cache.
+//  * argmax_kernel — greedy next token per row (first maximum, as argmax), also
+//    recorded into a token history at column *step_dev.
+#include "common.h"
+#include "internal.h"
+
+#include <limits.h>
+
+namespace cgpt {
+
+// --------------------------------------------------------------- skinny GEMM
+
+constexpr int kSkWaves = 8;
+constexpr int kSkUnroll = 8;
+
+__device__ __forceinline__ float bias_value(const void* bias, bool bf16, int n) {
+  return bf16 ? bf16_to_f32(static_cast<const bf16_t*>(bias)[n]) : static_cast<const float*>(bias)[n];
+}
+
+template <typename TIn, int MT, int EPI, typename TOut>
+__global__ __launch_bounds__(64 * kSkWaves) void gemm_skinny_kernel(
+    const TIn* __restrict__ A, const TIn* __restrict__ W, const void* __restrict__ bias,
+    bool bias_bf16, TOut* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldw,
+    int64_t ldc, bool vec_store) {
+  constexpr int EPC = 16 / sizeof(TIn);  // elements per 16-byte fragment
+  constexpr int KS = 4 * EPC;            // k per slab (4 lane groups)
+  constexpr int U = kSkUnroll;
+  __shared__ f32x4_t red[kSkWaves][MT][64];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n0 = blockIdx.x * 16;
+  const int r16 = lane & 15, g = lane >> 4;
+  // Rows past N / M are clamped (loaded, never stored).
+  const TIn* wrow = W + static_cast<int64_t>(min(n0 + r16, N - 1)) * ldw + g * EPC;
+  const TIn* arow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+    arow[mt] = A + static_cast<int64_t>(min(16 * mt + r16, M - 1)) * lda + g * EPC;
+
+  const int slabs = (K + KS - 1) / KS;
+  const int per = (slabs + kSkWaves - 1) / kSkWaves;
+  const int s0 = wave * per;
+  const int s1 = min(slabs, s0 + per);
+
+  f32x4_t acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int s = s0; s < s1; s += U) {
+    u32x4_t wf[U], af[U][MT];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      // This lane's chunk starts at k = (s+u)*KS + g*EPC (the row pointers
+      // already hold g*EPC); chunks past K or past this wave's range load
+      // the row's first chunk and are zeroed.
+      const int k = (s + u) * KS + g * EPC;
+      const bool ok = (s + u < s1) && (k < K);
+      const int off = ok ? (s + u) * KS : -g * EPC;
+      wf[u] = *reinterpret_cast<const u32x4_t*>(wrow + off);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) af[u][mt] = *reinterpret_cast<const u32x4_t*>(arow[mt] + off);
+      if (!ok) {
+        wf[u] = u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) af[u][mt] = u32x4_t{0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) Mfma<TIn>::run(wf[u], af[u][mt], acc[mt]);
+  }
+
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) red[wave][mt][lane] = acc[mt];
+  __syncthreads();
+  for (int mt = wave; mt < MT; mt += kSkWaves) {
+    f32x4_t t = red[0][mt][lane];
+#pragma unroll
+    for (int w = 1; w < kSkWaves; ++w) t += red[w][mt][lane];
+    const int m = 16 * mt + r16, n = n0 + 4 * g;
+    float v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float x = t[r];
+      if (EPI != CGPT_EPI_NONE) x += n + r < N ? bias_value(bias, bias_bf16, n + r) : 0.f;
+      if (EPI == CGPT_EPI_BIAS_GELU) x = gelu_tanh(x);
+      v[r] = x;
+    }
+    if (m < M && n < N) {
+      TOut* out = C + static_cast<int64_t>(m) * ldc + n;
+      if (vec_store && n + 3 < N) {
+        store4_out(out, v);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (n + r < N) Elem<TOut>::store(out + r, v[r]);
+      }
+    }
+  }
+}
+
+template <typename TIn, int EPI, typename TOut>
+static int launch_skinny_mt(const void* a, const void* w, const void* bias, bool bias_bf16, void* c,
+                            int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc,
+                            bool vec_store, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((N + 15) / 16)), block(64 * kSkWaves);
+  const TIn* A = static_cast<const TIn*>(a);
+  const TIn* W = static_cast<const TIn*>(w);
+  TOut* C = static_cast<TOut*>(c);
+  if (M <= 16)
+    hipLaunchKernelGGL((gemm_skinny_kernel<TIn, 1, EPI, TOut>), grid, block, 0, s, A, W, bias,
+                       bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store);
+  else if (M <= 32)
+    hipLaunchKernelGGL((gemm_skinny_kernel<TIn, 2, EPI, TOut>), grid, block, 0, s, A, W, bias,
+                       bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store);
+  else
+    hipLaunchKernelGGL((gemm_skinny_kernel<TIn, 4, EPI, TOut>), grid, block, 0, s, A, W, bias,
+                       bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store);
+  return hip_status(hipGetLastError());
+}
+
+template <typename TIn, typename TOut>
+static int launch_skinny_epi(int epi, const void* a, const void* w, const void* bias, bool bias_bf16,
+                             void* c, int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc,
+                             bool vec_store, hipStream_t s) {
+  switch (epi) {
+    case CGPT_EPI_NONE:
+      return launch_skinny_mt<TIn, CGPT_EPI_NONE, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, s);
+    case CGPT_EPI_BIAS:
+      return launch_skinny_mt<TIn, CGPT_EPI_BIAS, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, s);
+    case CGPT_EPI_BIAS_GELU:
+      return launch_skinny_mt<TIn, CGPT_EPI_BIAS_GELU, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, s);
+    default:
+      return CGPT_EINVAL;
+  }
+}
+
+int launch_gemm_skinny(bool bf16_in, int epilogue, const void* a, const void* w, const void* bias,
+                       bool bias_bf16, void* c, bool out_bf16, int M, int N, int K, int64_t lda,
+                       int64_t ldw, int64_t ldc, hipStream_t s) {
+  if (M > 64) return CGPT_ESHAPE;
+  const uintptr_t oa = out_bf16 ? 7 : 15;
+  const bool vec_store = ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(c) & oa) == 0;
+  if (bf16_in)
+    return out_bf16 ? launch_skinny_epi<bf16_t, bf16_t>(epilogue, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, s)
+                    : launch_skinny_epi<bf16_t, float>(epilogue, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, s);
+  return out_bf16 ? launch_skinny_epi<float, bf16_t>(epilogue, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, s)
+                  : launch_skinny_epi<float, float>(epilogue, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, s);
+}
+
+// ------------------------------------------------------- decode attention
+
+constexpr int kDecThreads = 256;
+constexpr int kDecWaves = kDecThreads / 64;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Block-wide reduction of one value per thread (sum or max); `scr` holds
+// kDecWaves floats.  Every thread returns the result.
+template <bool kMax>
+__device__ __forceinline__ float block_reduce(float v, float* scr) {
+  v = kMax ? wave_max(v) : wave_sum(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) scr[wave] = v;
+  __syncthreads();
+  float r = scr[0];
+#pragma unroll
+  for (int w = 1; w < kDecWaves; ++w) r = kMax ? fmaxf(r, scr[w]) : r + scr[w];
+  return r;
+}
+
+template <typename T> __device__ __forceinline__ float round_to(float x);
+template <> __device__ __forceinline__ float round_to<float>(float x) { return x; }
+template <> __device__ __forceinline__ float round_to<bf16_t>(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
+template <typename T>
+__global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(
+    const T* __restrict__ q, const T* __restrict__ kn, const T* __restrict__ vn, T* __restrict__ kc,
+    T* __restrict__ vc, T* __restrict__ o, int H, int hd, int Tmax, int pos_base,
+    const int* __restrict__ pos_dev, int64_t q_sb, int64_t q_sh, int64_t kn_sb, int64_t kn_sh,
+    int64_t vn_sb, int64_t vn_sh, int64_t c_sb, int64_t c_sh, int64_t c_st, int64_t o_sb,
+    int64_t o_sh, float scale_log2, int* err_flag) {
+  constexpr int EPV = Elem<T>::kVec;  // elements per 16-byte vector
+  extern __shared__ float dsm[];
+  float* qs = dsm;                     // hd
+  float* sc = qs + hd;                 // Tmax scores, then probabilities
+  float* part = sc + Tmax;             // kDecThreads partial outputs
+  float* scr = part + kDecThreads;     // kDecWaves
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x / H, h = blockIdx.x % H;
+  int pos = pos_base + (pos_dev != nullptr ? *pos_dev : 0);
+  if (pos < 0 || pos >= Tmax) {
+    if (err_flag != nullptr && tid == 0) *err_flag = 1;
+    pos = pos < 0 ? 0 : Tmax - 1;
+  }
+  const int Tk = pos + 1;
+  T* kcb = kc + b * c_sb + h * c_sh;
+  T* vcb = vc + b * c_sb + h * c_sh;
+  const T* knb = kn + b * kn_sb + h * kn_sh;
+  const T* vnb = vn + b * vn_sb + h * vn_sh;
+  const T* qb = q + b * q_sb + h * q_sh;
+  for (int d = tid; d < hd; d += kDecThreads) {
+    kcb[pos * c_st + d] = knb[d];
+    vcb[pos * c_st + d] = vnb[d];
+    qs[d] = Elem<T>::load(qb + d);
+  }
+  __syncthreads();  // the appended row and q are visible to the whole block
+
+  float mx = -INFINITY;
+  for (int j = tid; j < Tk; j += kDecThreads) {
+    const T* kr = kcb + j * c_st;
+    float s = 0.f;
+    for (int d = 0; d < hd; d += EPV) {
+      float kv[EPV];
+      load_vec(kr + d, kv);
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) s = fmaf(qs[d + e], kv[e], s);
+    }
+    s *= scale_log2;
+    sc[j] = s;
+    mx = fmaxf(mx, s);
+  }
+  mx = block_reduce<true>(mx, scr);
+  float sum = 0.f;
+  for (int j = tid; j < Tk; j += kDecThreads) {
+    const float p = __builtin_amdgcn_exp2f(sc[j] - mx);
+    sc[j] = p;
+    sum += p;
+  }
+  sum = block_reduce<false>(sum, scr);  // its barriers also publish sc
+
+  // P V: thread (group gi, dim d) sums keys gi, gi + G, ...; P is rounded to
+  // the storage type before the product, as in the prefill kernel.
+  const int G = kDecThreads / hd, gi = tid / hd, d = tid % hd;
+  float acc = 0.f;
+  if (gi < G)
+    for (int j = gi; j < Tk; j += G) acc = fmaf(round_to<T>(sc[j]), Elem<T>::load(vcb + j * c_st + d), acc);
+  part[tid] = acc;
+  __syncthreads();
+  if (tid < hd) {
+    float t = 0.f;
+    for (int k = 0; k < G; ++k) t += part[k * hd + tid];
+    Elem<T>::store(o + b * o_sb + h * o_sh + tid, t / sum);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void kv_store_kernel(
+    const T* __restrict__ k, const T* __restrict__ v, T* __restrict__ kc, T* __restrict__ vc, int H,
+    int Tn, int hd, int pos0, int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t v_sb, int64_t v_sh,
+    int64_t v_st, int64_t c_sb, int64_t c_sh, int64_t c_st, int64_t total_chunks) {
+  constexpr int EPV = Elem<T>::kVec;
+  const int cpr = hd / EPV;  // 16-byte chunks per row
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total_chunks;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int c = static_cast<int>(i % cpr);
+    int64_t r = i / cpr;
+    const int t = static_cast<int>(r % Tn);
+    r /= Tn;
+    const int h = static_cast<int>(r % H);
+    const int64_t b = r / H;
+    const int64_t dst = b * c_sb + h * c_sh + static_cast<int64_t>(pos0 + t) * c_st + c * EPV;
+    *reinterpret_cast<u32x4_t*>(kc + dst) =
+        *reinterpret_cast<const u32x4_t*>(k + b * k_sb + h * k_sh + t * k_st + c * EPV);
+    *reinterpret_cast<u32x4_t*>(vc + dst) =
+        *reinterpret_cast<const u32x4_t*>(v + b * v_sb + h * v_sh + t * v_st + c * EPV);
+  }
+}
+
+// ------------------------------------------------------------------- argmax
+
+template <typename T>
+__global__ __launch_bounds__(256) void argmax_kernel(const T* __restrict__ x, int64_t ld, int cols,
+                                                     int64_t* __restrict__ ids, int64_t* __restrict__ hist,
+                                                     int64_t hist_ld, const int* __restrict__ step_dev) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  const T* row = x + static_cast<int64_t>(blockIdx.x) * ld;
+  float best = -INFINITY;
+  int bi = INT_MAX;
+  for (int c = threadIdx.x; c < cols; c += 256) {
+    const float v = Elem<T>::load(row + c);
+    if (v > best) {  // ascending scan: the first maximum wins
+      best = v;
+      bi = c;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(best, off, 64);
+    const int oi = __shfl_xor(bi, off, 64);
+    if (ov > best || (ov == best && oi < bi)) {
+      best = ov;
+      bi = oi;
+    }
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    sv[wave] = best;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; ++w)
+      if (sv[w] > best || (sv[w] == best && si[w] < bi)) {
+        best = sv[w];
+        bi = si[w];
+      }
+    if (bi == INT_MAX) bi = 0;  // a row of NaN or -inf only
+    ids[blockIdx.x] = bi;
+    if (hist != nullptr) hist[blockIdx.x * hist_ld + (step_dev != nullptr ? *step_dev : 0)] = bi;
+  }
+}
+
+}  // namespace cgpt
+
+using namespace cgpt;
+
+extern "C" int cgpt_attention_decode(const void* q, const void* k_new, const void* v_new,
+                                     void* k_cache, void* v_cache, void* o, int64_t B, int64_t H,
+                                     int64_t head_dim, int64_t t_max, int64_t pos_base,
+                                     const int* pos_dev, int64_t q_sb, int64_t q_sh,
+                                     int64_t kn_sb, int64_t kn_sh, int64_t vn_sb, int64_t vn_sh,
+                                     int64_t c_sb, int64_t c_sh, int64_t c_st, int64_t o_sb,
+                                     int64_t o_sh, float scale, int dtype, int* err_flag,
+                                     void* stream) {
+  if (B < 0 || H <= 0 || head_dim <= 0 || t_max <= 0) return CGPT_EINVAL;
+  if (B == 0) return CGPT_OK;
+  if (!q || !k_new || !v_new || !k_cache || !v_cache || !o) return CGPT_EINVAL;
+  if (dtype != CGPT_F32 && dtype != CGPT_BF16) return CGPT_EDTYPE;
+  const int epv = dtype == CGPT_F32 ? 4 : 8;
+  if (head_dim > kDecThreads || kDecThreads % head_dim != 0 || head_dim % epv != 0) return CGPT_ESHAPE;
+  if (t_max > 16384 || B * H > 0x7fffffff) return CGPT_ESHAPE;
+  // Cache rows are read as 16-byte vectors.
+  if (c_st % epv != 0 || c_sh % epv != 0 || c_sb % epv != 0 || c_st < head_dim) return CGPT_EINVAL;
+  if ((reinterpret_cast<uintptr_t>(k_cache) & 15) || (reinterpret_cast<uintptr_t>(v_cache) & 15))
+    return CGPT_EINVAL;
+  if (pos_dev == nullptr && (pos_base < 0 || pos_base >= t_max)) return CGPT_EINVAL;
+  const size_t smem = (static_cast<size_t>(head_dim) + t_max + kDecThreads + kDecWaves) * sizeof(float);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const float sl2 = scale * 1.4426950408889634f;
+  const int hh = static_cast<int>(H), hd = static_cast<int>(head_dim), tm = static_cast<int>(t_max);
+  const int pb = static_cast<int>(pos_base);
+  if (dtype == CGPT_BF16)
+    hipLaunchKernelGGL(attn_decode_kernel<bf16_t>, dim3(static_cast<unsigned>(B * H)), dim3(kDecThreads),
+                       smem, s, static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k_new),
+                       static_cast<const bf16_t*>(v_new), static_cast<bf16_t*>(k_cache),
+                       static_cast<bf16_t*>(v_cache), static_cast<bf16_t*>(o), hh, hd, tm, pb, pos_dev,
+                       q_sb, q_sh, kn_sb, kn_sh, vn_sb, vn_sh, c_sb, c_sh, c_st, o_sb, o_sh, sl2, err_flag);
+  else
+    hipLaunchKernelGGL(attn_decode_kernel<float>, dim3(static_cast<unsigned>(B * H)), dim3(kDecThreads),
+                       smem, s, static_cast<const float*>(q), static_cast<const float*>(k_new),
+                       static_cast<const float*>(v_new), static_cast<float*>(k_cache),
+                       static_cast<float*>(v_cache), static_cast<float*>(o), hh, hd, tm, pb, pos_dev,
+                       q_sb, q_sh, kn_sb, kn_sh, vn_sb, vn_sh, c_sb, c_sh, c_st, o_sb, o_sh, sl2, err_flag);
+  return hip_status(hipGetLastError());
+}
+
+extern "C" int cgpt_kv_store(const void* k, const void* v, void* k_cache, void* v_cache, int64_t B,
+                             int64_t H, int64_t T, int64_t head_dim, int64_t pos0, int64_t t_max,
+                             int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t v_sb, int64_t v_sh,
+                             int64_t v_st, int64_t c_sb, int64_t c_sh, int64_t c_st, int dtype,
+                             void* stream) {
+  if (B < 0 || H <= 0 || T < 0 || head_dim <= 0 || pos0 < 0) return CGPT_EINVAL;
+  if (B == 0 || T == 0) return CGPT_OK;
+  if (!k || !v || !k_cache || !v_cache) return CGPT_EINVAL;
+  if (pos0 + T > t_max) return CGPT_ESHAPE;
+  if (dtype != CGPT_F32 && dtype != CGPT_BF16) return CGPT_EDTYPE;
+  const int epv = dtype == CGPT_F32 ? 4 : 8;
+  if (head_dim % epv != 0) return CGPT_ESHAPE;
+  for (int64_t st : {k_sb, k_sh, k_st, v_sb, v_sh, v_st, c_sb, c_sh, c_st})
+    if (st % epv != 0) return CGPT_EINVAL;
+  for (const void* p : {k, v, static_cast<const void*>(k_cache), static_cast<const void*>(v_cache)})
+    if (reinterpret_cast<uintptr_t>(p) & 15) return CGPT_EINVAL;
+  const int64_t chunks = B * H * T * (head_dim / epv);
+  const int64_t want = (chunks + 255) / 256;
+  const unsigned grid = static_cast<unsigned>(want < 4096 ? want : 4096);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int hh = static_cast<int>(H), tt = static_cast<int>(T), hd = static_cast<int>(head_dim);
+  const int p0 = static_cast<int>(pos0);
+  if (dtype == CGPT_BF16)
+    hipLaunchKernelGGL(kv_store_kernel<bf16_t>, dim3(grid), dim3(256), 0, s, static_cast<const bf16_t*>(k),
+                       static_cast<const bf16_t*>(v), static_cast<bf16_t*>(k_cache),
+                       static_cast<bf16_t*>(v_cache), hh, tt, hd, p0, k_sb, k_sh, k_st, v_sb, v_sh, v_st,
+                       c_sb, c_sh, c_st, chunks);
+  else
+    hipLaunchKernelGGL(kv_store_kernel<float>, dim3(grid), dim3(256), 0, s, static_cast<const float*>(k),
+                       static_cast<const float*>(v), static_cast<float*>(k_cache),
+                       static_cast<float*>(v_cache), hh, tt, hd, p0, k_sb, k_sh, k_st, v_sb, v_sh, v_st,
+                       c_sb, c_sh, c_st, chunks);
+  return hip_status(hipGetLastError());
+}
+
+extern "C" int cgpt_argmax(const void* x, int64_t rows, int64_t cols, int64_t ld, int dtype,
+                           int64_t* ids, int64_t* hist, int64_t hist_ld, const int* step_dev,
+                           void* stream) {
+  if (rows < 0 || cols <= 0 || ld < cols) return CGPT_EINVAL;
+  if (rows == 0) return CGPT_OK;
+  if (!x || !ids || (hist != nullptr && hist_ld <= 0)) return CGPT_EINVAL;
+  if (rows > 0x7fffffff || cols > 0x7fffffff) return CGPT_ESHAPE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int c = static_cast<int>(cols);
+  if (dtype == CGPT_F32)
+    hipLaunchKernelGGL(argmax_kernel<float>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s,
+                       static_cast<const float*>(x), ld, c, ids, hist, hist_ld, step_dev);
+  else if (dtype == CGPT_BF16)
+    hipLaunchKernelGGL(argmax_kernel<bf16_t>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s,
+                       static_cast<const bf16_t*>(x), ld, c, ids, hist, hist_ld, step_dev);
+  else
+    return CGPT_EDTYPE;
+  return hip_status(hipGetLastError());
+}

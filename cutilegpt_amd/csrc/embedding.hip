@@ -1,6 +1,8 @@
 // Token + position embedding gather (HBM-bound, one wavefront per token).
 //
-// out[i, :] = wte[idx[i], :] (+ wpe[pos0 + i % T, :]); lane l of the wave moves
+// out[i, :] = wte[idx[i], :] (+ wpe[pos0 + i % T, :], or wpe[pos0 + *pos_dev, :]
+// for every token when the position comes from device memory, as in a decode
+// step replayed from one captured launch sequence); lane l of the wave moves
 // columns [4(64c + l), 4(64c + l) + 4) for each 256-column chunk c, so each row
 // is read and written with contiguous, fully coalesced spans.  Out-of-range
 // ids/positions are clamped (no out-of-bounds read is possible) and reported
@@ -30,7 +32,7 @@ template <typename TW, typename TO>
 __global__ __launch_bounds__(kEmbThreads) void embedding_kernel(
     const int64_t* __restrict__ idx, const TW* __restrict__ wte, const TW* __restrict__ wpe,
     TO* __restrict__ out, int64_t n_tokens, int64_t T, int D, int64_t vocab, int64_t pos0,
-    int64_t n_pos, int* err_flag) {
+    const int* __restrict__ pos_dev, int64_t n_pos, int* err_flag) {
   const int lane = threadIdx.x & 63;
   const int64_t i = static_cast<int64_t>(blockIdx.x) * kEmbTokensPerBlock + (threadIdx.x >> 6);
   if (i >= n_tokens) return;
@@ -40,7 +42,7 @@ __global__ __launch_bounds__(kEmbThreads) void embedding_kernel(
     bad = true;
     id = id < 0 ? 0 : vocab - 1;
   }
-  int64_t pos = pos0 + i % T;
+  int64_t pos = pos0 + (pos_dev != nullptr ? static_cast<int64_t>(*pos_dev) : i % T);
   if (wpe != nullptr && (pos < 0 || pos >= n_pos)) {
     bad = true;
     pos = pos < 0 ? 0 : n_pos - 1;
@@ -65,20 +67,20 @@ __global__ __launch_bounds__(kEmbThreads) void embedding_kernel(
 template <typename TW, typename TO>
 static int launch_emb(const int64_t* idx, const void* wte, const void* wpe, void* out,
                       int64_t n_tokens, int64_t T, int D, int64_t vocab, int64_t pos0,
-                      int64_t n_pos, int* err, hipStream_t s) {
+                      const int* pos_dev, int64_t n_pos, int* err, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>((n_tokens + kEmbTokensPerBlock - 1) / kEmbTokensPerBlock));
   hipLaunchKernelGGL((embedding_kernel<TW, TO>), grid, dim3(kEmbThreads), 0, s, idx,
                      static_cast<const TW*>(wte), static_cast<const TW*>(wpe),
-                     static_cast<TO*>(out), n_tokens, T, D, vocab, pos0, n_pos, err);
+                     static_cast<TO*>(out), n_tokens, T, D, vocab, pos0, pos_dev, n_pos, err);
   return hip_status(hipGetLastError());
 }
 
 }  // namespace cgpt
 
-extern "C" int cgpt_embedding(const int64_t* idx, const void* wte, const void* wpe, void* out,
-                              int64_t n_tokens, int64_t T, int64_t D, int64_t vocab,
-                              int64_t pos0, int64_t n_pos, int w_dtype, int out_dtype,
-                              int* err_flag, void* stream) {
+static int embedding_impl(const int64_t* idx, const void* wte, const void* wpe, void* out,
+                          int64_t n_tokens, int64_t T, int64_t D, int64_t vocab, int64_t pos0,
+                          const int* pos_dev, int64_t n_pos, int w_dtype, int out_dtype,
+                          int* err_flag, void* stream) {
   using namespace cgpt;
   if (n_tokens < 0 || D <= 0 || vocab <= 0) return CGPT_EINVAL;
   if (n_tokens == 0) return CGPT_OK;
@@ -93,12 +95,29 @@ extern "C" int cgpt_embedding(const int64_t* idx, const void* wte, const void* w
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int d = static_cast<int>(D);
   if (w_dtype == CGPT_F32 && out_dtype == CGPT_F32)
-    return launch_emb<float, float>(idx, wte, wpe, out, n_tokens, T, d, vocab, pos0, n_pos, err_flag, s);
+    return launch_emb<float, float>(idx, wte, wpe, out, n_tokens, T, d, vocab, pos0, pos_dev, n_pos, err_flag, s);
   if (w_dtype == CGPT_BF16 && out_dtype == CGPT_F32)
-    return launch_emb<bf16_t, float>(idx, wte, wpe, out, n_tokens, T, d, vocab, pos0, n_pos, err_flag, s);
+    return launch_emb<bf16_t, float>(idx, wte, wpe, out, n_tokens, T, d, vocab, pos0, pos_dev, n_pos, err_flag, s);
   if (w_dtype == CGPT_BF16 && out_dtype == CGPT_BF16)
-    return launch_emb<bf16_t, bf16_t>(idx, wte, wpe, out, n_tokens, T, d, vocab, pos0, n_pos, err_flag, s);
+    return launch_emb<bf16_t, bf16_t>(idx, wte, wpe, out, n_tokens, T, d, vocab, pos0, pos_dev, n_pos, err_flag, s);
   if (w_dtype == CGPT_F32 && out_dtype == CGPT_BF16)
-    return launch_emb<float, bf16_t>(idx, wte, wpe, out, n_tokens, T, d, vocab, pos0, n_pos, err_flag, s);
+    return launch_emb<float, bf16_t>(idx, wte, wpe, out, n_tokens, T, d, vocab, pos0, pos_dev, n_pos, err_flag, s);
   return CGPT_EDTYPE;
+}
+
+extern "C" int cgpt_embedding(const int64_t* idx, const void* wte, const void* wpe, void* out,
+                              int64_t n_tokens, int64_t T, int64_t D, int64_t vocab,
+                              int64_t pos0, int64_t n_pos, int w_dtype, int out_dtype,
+                              int* err_flag, void* stream) {
+  return embedding_impl(idx, wte, wpe, out, n_tokens, T, D, vocab, pos0, nullptr, n_pos, w_dtype,
+                        out_dtype, err_flag, stream);
+}
+
+extern "C" int cgpt_embedding_at(const int64_t* idx, const void* wte, const void* wpe, void* out,
+                                 int64_t n_tokens, int64_t D, int64_t vocab, int64_t pos_base,
+                                 const int* pos_dev, int64_t n_pos, int w_dtype, int out_dtype,
+                                 int* err_flag, void* stream) {
+  if (pos_dev == nullptr) return CGPT_EINVAL;
+  return embedding_impl(idx, wte, wpe, out, n_tokens, 1, D, vocab, pos_base, pos_dev, n_pos,
+                        w_dtype, out_dtype, err_flag, stream);
 }

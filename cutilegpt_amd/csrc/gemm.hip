@@ -26,33 +26,12 @@
 //  * gemm_pipe_kernel: bf16 direct-to-LDS multi-stage pipeline, persistent
 //    over tiles (see the comment above it).
 #include "common.h"
+#include "internal.h"
 
 namespace cgpt {
 
 constexpr int kGroupM = 8;
 constexpr int kNumXcd = 8;
-
-template <typename T> struct Mfma;
-template <> struct Mfma<bf16_t> {
-  __device__ static void run(const u32x4_t& a, const u32x4_t& b, f32x4_t& c) {
-    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-  }
-};
-template <> struct Mfma<float> {
-  __device__ static void run(const u32x4_t& a, const u32x4_t& b, f32x4_t& c) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[j]), __uint_as_float(b[j]), c, 0,
-                                               0, 0);
-  }
-};
-
-__device__ __forceinline__ void store4_out(float* p, const float* v) { store_vec(p, v); }
-__device__ __forceinline__ void store4_out(bf16_t* p, const float* v) {
-  u32x2_t u = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-  *reinterpret_cast<u32x2_t*>(p) = u;
-}
 
 #if defined(__HIP_DEVICE_COMPILE__)
 // Four consecutive outputs through a buffer resource: a store whose byte
@@ -845,6 +824,13 @@ extern "C" int cgpt_gemm(const void* a, const void* w, const void* bias, void* c
     return CGPT_EINVAL;
   if (epilogue != CGPT_EPI_NONE && (reinterpret_cast<uintptr_t>(bias) & 15)) return CGPT_EINVAL;
   const int nt = bf16 ? kNumBf16Tiles : kNumF32Tiles;
+  if (tile == CGPT_TILE_AUTO && M <= 64) tile = CGPT_TILE_SKINNY;
+  if (tile == CGPT_TILE_SKINNY) {
+    if (M > 64) return CGPT_ESHAPE;
+    return launch_gemm_skinny(bf16, epilogue, a, w, bias, bias_dtype == CGPT_BF16, c,
+                              out_dtype == CGPT_BF16, static_cast<int>(M), static_cast<int>(N),
+                              static_cast<int>(K), lda, ldw, ldc, static_cast<hipStream_t>(stream));
+  }
   if (tile == CGPT_TILE_AUTO)
     tile = auto_tile(bf16, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K));
   if (tile < 0 || tile >= nt) return CGPT_EINVAL;

@@ -1,0 +1,183 @@
+"""KV-cache incremental decoding for CutileGPT (greedy or sampled).
+
+The reference's ``generate`` (``cutile_gpt/models/gpt.py:185-229``) re-runs the
+whole forward on the growing prefix for every new token.  Here a prompt is run
+once (prefill) while its keys and values are stored into a per-layer cache,
+and every further token costs one step over B rows:
+
+    embedding at position pos        cgpt_embedding_at (pos read on device)
+    per layer: LN, QKV GEMM          cgpt_add_layernorm, cgpt_gemm (skinny, M = B)
+               attention             cgpt_attention_decode (appends k, v at pos)
+               proj, LN, fc+GELU, proj
+    LN_f, LM head                    cgpt_gemm (skinny, N = vocab)
+    greedy token                     cgpt_argmax (also written to the history)
+
+Everything a step reads or writes lives in buffers allocated once per
+``generate`` call and the position is a device counter, so the greedy step is
+captured once as a HIP graph and replayed for every token.
+
+Cache layout, per layer: k and v of shape (B, H, t_max, head_dim) in the model
+dtype, t_max = prompt length + new tokens (<= block_size).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+_DT = {torch.float32: _lib.CGPT_F32, torch.bfloat16: _lib.CGPT_BF16}
+
+
+class KVCache:
+    """Keys and values of every layer: ``k[i]``, ``v[i]`` of shape (B, H, t_max, hd)."""
+
+    def __init__(self, n_layer: int, B: int, H: int, t_max: int, hd: int, dtype: torch.dtype,
+                 device: torch.device):
+        self.t_max = t_max
+        self.k = torch.empty((n_layer, B, H, t_max, hd), dtype=dtype, device=device)
+        self.v = torch.empty((n_layer, B, H, t_max, hd), dtype=dtype, device=device)
+
+    def strides(self):
+        """(batch, head, time) element strides of one layer's k or v."""
+        s = self.k[0].stride()
+        return s[0], s[1], s[2]
+
+
+class DecodeSession:
+    """Buffers, cache and device counters of one batched generation."""
+
+    def __init__(self, model, B: int, t0: int, max_new: int):
+        cfg = model.config
+        if t0 + max_new > cfg.block_size:
+            raise ValueError(f"prompt {t0} + {max_new} new tokens exceeds block_size {cfg.block_size}")
+        if B > 64:
+            raise ValueError("KV-cache decoding supports at most 64 sequences per batch")
+        self.model = model
+        self.B, self.t0, self.max_new = B, t0, max_new
+        dev, act = model.device, model.dtype
+        D, H, V = cfg.n_embd, cfg.n_head, cfg.vocab_size
+        self.hd = D // H
+        self.cache = KVCache(cfg.n_layer, B, H, t0 + max_new, self.hd, act, dev)
+        self.ids = torch.zeros(B, dtype=torch.int64, device=dev)
+        self.step = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.hist = torch.zeros((B, max_new), dtype=torch.int64, device=dev)
+        self.x = torch.empty((B, D), dtype=torch.float32, device=dev)
+        self.h = torch.empty((B, D), dtype=act, device=dev)
+        self.qkv = torch.empty((B, 3 * D), dtype=act, device=dev)
+        self.att = torch.empty((B, D), dtype=act, device=dev)
+        self.delta = torch.empty((B, D), dtype=act, device=dev)
+        self.f = torch.empty((B, 4 * D), dtype=act, device=dev)
+        self.logits = torch.empty((B, V), dtype=model.logits_dtype, device=dev)
+        self.err = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.graph: Optional[torch.cuda.CUDAGraph] = None
+
+    # ----------------------------------------------------------------- prefill
+
+    def prefill(self, idx: torch.Tensor) -> None:
+        """Run the prompt, fill the cache; leaves the last position's logits in
+        ``self.logits``."""
+        self.model._forward(idx, cache=self.cache, logits_out=self.logits)
+
+    def greedy_first(self) -> None:
+        """First new token (history column 0) from the prefill logits."""
+        lib = _lib.load()
+        s = torch.cuda.current_stream(self.model.device).cuda_stream
+        V = self.model.config.vocab_size
+        _lib.check(lib.cgpt_argmax(self.logits.data_ptr(), self.B, V, V, _DT[self.logits.dtype],
+                                   self.ids.data_ptr(), self.hist.data_ptr(), self.max_new, None, s),
+                   "argmax")
+
+    # -------------------------------------------------------------------- step
+
+    def step_logits(self) -> None:
+        """One step for the tokens in ``self.ids`` at position t0 + step:
+        appends to the cache and writes next-token logits to ``self.logits``."""
+        m = self.model
+        cfg = m.config
+        lib = _lib.load()
+        chk = _lib.check
+        W = m.weights
+        B, D, H, V, hd = self.B, cfg.n_embd, cfg.n_head, cfg.vocab_size, self.hd
+        ac = _DT[m.dtype]
+        f32 = _lib.CGPT_F32
+        skinny = _lib.TILE_SKINNY
+        s = torch.cuda.current_stream(m.device).cuda_stream
+        px, ph, pq, pa, pd, pf = (t.data_ptr() for t in (self.x, self.h, self.qkv, self.att,
+                                                         self.delta, self.f))
+        pstep = self.step.data_ptr()
+        esz = self.qkv.element_size()
+
+        def gemm(a_ptr, w, b, c_ptr, n, k, epi, out_code):
+            chk(lib.cgpt_gemm(a_ptr, w.data_ptr(), None if b is None else b.data_ptr(), c_ptr,
+                              B, n, k, k, w.stride(0), n, ac, ac, out_code, epi, skinny, s), "gemm")
+
+        def add_ln(delta_ptr, wk):
+            chk(lib.cgpt_add_layernorm(px, delta_ptr, px if delta_ptr else None,
+                                       W[wk + ".weight"].data_ptr(), W[wk + ".bias"].data_ptr(),
+                                       ph, B, D, 1e-5, f32, ac, ac, ac, s), "add_layernorm")
+
+        chk(lib.cgpt_embedding_at(self.ids.data_ptr(), W["wte"].data_ptr(), W["wpe"].data_ptr(),
+                                  px, B, D, V, self.t0, pstep, cfg.block_size, ac, f32,
+                                  self.err.data_ptr(), s), "embedding_at")
+        add_ln(None, "h.0.ln_1")
+        csb, csh, cst = self.cache.strides()
+        t_max = self.cache.t_max
+        scale = 1.0 / math.sqrt(hd)
+        for i in range(cfg.n_layer):
+            p = f"h.{i}."
+            gemm(ph, W[p + "attn.c_attn.weight"], W[p + "attn.c_attn.bias"], pq, 3 * D, D,
+                 _lib.EPI_BIAS, ac)
+            chk(lib.cgpt_attention_decode(pq, pq + D * esz, pq + 2 * D * esz,
+                                          self.cache.k[i].data_ptr(), self.cache.v[i].data_ptr(),
+                                          pa, B, H, hd, t_max, self.t0, pstep,
+                                          3 * D, hd, 3 * D, hd, 3 * D, hd, csb, csh, cst, D, hd,
+                                          scale, ac, self.err.data_ptr(), s), "attention_decode")
+            gemm(pa, W[p + "attn.c_proj.weight"], W[p + "attn.c_proj.bias"], pd, D, D,
+                 _lib.EPI_BIAS, ac)
+            add_ln(pd, p + "ln_2")
+            gemm(ph, W[p + "mlp.c_fc.weight"], W[p + "mlp.c_fc.bias"], pf, 4 * D, D,
+                 _lib.EPI_BIAS_GELU, ac)
+            gemm(pf, W[p + "mlp.c_proj.weight"], W[p + "mlp.c_proj.bias"], pd, D, 4 * D,
+                 _lib.EPI_BIAS, ac)
+            add_ln(pd, f"h.{i + 1}.ln_1" if i + 1 < cfg.n_layer else "ln_f")
+        gemm(ph, W["lm_head.weight"], None, self.logits.data_ptr(), V, D, _lib.EPI_NONE,
+             _DT[self.logits.dtype])
+
+    def greedy_step(self) -> None:
+        """``step_logits`` + argmax into ``ids`` and history column step + 1,
+        then advance the step counter."""
+        self.step_logits()
+        lib = _lib.load()
+        s = torch.cuda.current_stream(self.model.device).cuda_stream
+        V = self.model.config.vocab_size
+        _lib.check(lib.cgpt_argmax(self.logits.data_ptr(), self.B, V, V, _DT[self.logits.dtype],
+                                   self.ids.data_ptr(), self.hist.data_ptr() + 8, self.max_new,
+                                   self.step.data_ptr(), s), "argmax")
+        self.step.add_(1)
+
+    def run_greedy(self, use_graph: bool = True) -> torch.Tensor:
+        """Generate ``max_new`` tokens after ``prefill``; returns (B, max_new)."""
+        self.greedy_first()
+        n = self.max_new - 1
+        if n <= 0:
+            return self.hist
+        if not use_graph or n < 3:
+            for _ in range(n):
+                self.greedy_step()
+            return self.hist
+        self.greedy_step()  # eager first step (also loads every kernel)
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(self.model.device)
+        side.wait_stream(torch.cuda.current_stream(self.model.device))
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(g, stream=side):
+                self.greedy_step()
+        torch.cuda.current_stream(self.model.device).wait_stream(side)
+        self.graph = g
+        for _ in range(n - 1):
+            g.replay()
+        return self.hist

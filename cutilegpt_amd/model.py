@@ -144,6 +144,14 @@ class CutileGPT:
         ``probe(tag, False)`` right after each kernel launch (tags: embedding,
         ln, gemm_qkv, attention, gemm_proj, gemm_fc_gelu, gemm_mlp_proj,
         lm_head) — a hook for timing individual launches with stream events."""
+        return self._forward(idx, probe=probe), None
+
+    def _forward(self, idx: torch.Tensor, probe=None, cache=None,
+                 logits_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Forward body.  ``cache`` (a ``decode.KVCache``): also store every
+        layer's keys and values at positions 0..T-1.  ``logits_out`` (B, vocab):
+        compute the LM head for the last position of each sequence only, into
+        that tensor, and return it."""
         B, T = idx.shape
         cfg = self.config
         assert T <= cfg.block_size, f"Sequence length {T} > block_size {cfg.block_size}"
@@ -168,7 +176,8 @@ class CutileGPT:
         att = torch.empty((M, D), dtype=act, device=dev)
         delta = torch.empty((M, D), dtype=act, device=dev)
         f = torch.empty((M, 4 * D), dtype=act, device=dev)
-        logits = torch.empty((M, V), dtype=self.logits_dtype, device=dev)
+        logits = (torch.empty((M, V), dtype=self.logits_dtype, device=dev)
+                  if logits_out is None else None)
         px, ph, pq, pa, pd, pf = (t.data_ptr() for t in (x, h, qkv, att, delta, f))
 
         mark = probe if probe is not None else (lambda tag, start: None)
@@ -201,6 +210,11 @@ class CutileGPT:
             gemm("gemm_qkv", ph, W[p + "attn.c_attn.weight"], W[p + "attn.c_attn.bias"], pq,
                  3 * D, D, _lib.EPI_BIAS, ac)
             esz = qkv.element_size()
+            if cache is not None:
+                csb, csh, cst = cache.strides()
+                chk(lib.cgpt_kv_store(pq + D * esz, pq + 2 * D * esz, cache.k[i].data_ptr(),
+                                      cache.v[i].data_ptr(), B, H, T, hd, 0, cache.t_max,
+                                      *st_qkv, *st_qkv, csb, csh, cst, ac, s), "kv_store")
             mark("attention", True)
             chk(lib.cgpt_attention_fwd(pq, pq + D * esz, pq + 2 * D * esz, pa, B, H, T, T, hd,
                                        *st_qkv, *st_qkv, *st_qkv, *st_o, scale, 1, ac, s),
@@ -214,9 +228,18 @@ class CutileGPT:
             gemm("gemm_mlp_proj", pf, W[p + "mlp.c_proj.weight"], W[p + "mlp.c_proj.bias"], pd,
                  D, 4 * D, _lib.EPI_BIAS, ac)
             add_ln(pd, f"h.{i + 1}.ln_1" if i + 1 < cfg.n_layer else "ln_f")
+        if logits_out is not None:
+            # Last position of each sequence: rows b*T + T-1 of h, stride T*D.
+            mark("lm_head", True)
+            chk(lib.cgpt_gemm(ph + (T - 1) * D * h.element_size(), W["lm_head.weight"].data_ptr(),
+                              None, logits_out.data_ptr(), B, V, D, T * D,
+                              W["lm_head.weight"].stride(0), V, ac, ac, _DT[logits_out.dtype],
+                              _lib.EPI_NONE, _lib.TILE_AUTO, s), "lm_head")
+            mark("lm_head", False)
+            return logits_out
         gemm("lm_head", ph, W["lm_head.weight"], None, logits.data_ptr(), V, D, _lib.EPI_NONE,
              _DT[self.logits_dtype])
-        return logits.view(B, T, V), None
+        return logits.view(B, T, V)
 
     def input_errors(self) -> bool:
         """True if any forward so far saw a token id outside the vocabulary
@@ -227,26 +250,61 @@ class CutileGPT:
 
     @torch.inference_mode()
     def generate(self, idx: torch.Tensor, max_new_tokens: int, temperature: float = 1.0,
-                 top_k: Optional[int] = None) -> torch.Tensor:
-        """Autoregressive continuation; restates ``cutile_gpt/models/gpt.py:185-229``
-        (full forward per token on the last block_size tokens, temperature,
-        top-k masking, sampling).  ``top_k=1`` is greedy decoding."""
+                 top_k: Optional[int] = None, use_cache: bool = True,
+                 use_graph: bool = True) -> torch.Tensor:
+        """Autoregressive continuation with the semantics of
+        ``cutile_gpt/models/gpt.py:185-229``: temperature, top-k masking, then
+        sampling; ``top_k=1`` is greedy decoding.
+
+        With ``use_cache`` (and prompt + new tokens within block_size, at most
+        64 sequences) the prompt is run once and each new token costs one
+        KV-cache step (``decode.DecodeSession``); greedy steps run entirely on
+        the device and are replayed from one captured HIP graph when
+        ``use_graph``.  Otherwise every token re-runs the full forward on the
+        last block_size tokens, as the reference does."""
         idx = self._prepare_idx(idx)
+        B, T0 = idx.shape
+        if max_new_tokens <= 0:
+            return idx
+        if use_cache and T0 + max_new_tokens <= self.config.block_size and B <= 64:
+            from .decode import DecodeSession
+
+            sess = DecodeSession(self, B, T0, max_new_tokens)
+            sess.prefill(idx)
+            if top_k == 1:
+                new = sess.run_greedy(use_graph=use_graph)
+                return torch.cat([idx, new], dim=1)
+            out = []
+            for t in range(max_new_tokens):
+                if t > 0:
+                    sess.step_logits()
+                nxt = self._sample(sess.logits, temperature, top_k)
+                out.append(nxt)
+                sess.ids.copy_(nxt.view(-1))
+                if t > 0:
+                    sess.step.add_(1)
+            return torch.cat([idx] + out, dim=1)
         for _ in range(max_new_tokens):
             cond = idx if idx.shape[1] <= self.config.block_size else idx[:, -self.config.block_size:]
-            logits, _ = self.forward(cond)
-            logits = logits[:, -1, :].float() / temperature
-            if top_k is not None:
-                k = min(top_k, logits.shape[-1])
-                kth = torch.topk(logits, k, dim=-1).values[:, -1:]
-                logits = logits.masked_fill(logits < kth, float("-inf"))
-            if top_k == 1:
-                nxt = logits.argmax(-1, keepdim=True)
-            else:
-                probs = torch.softmax(logits, dim=-1)
-                nxt = torch.multinomial(probs, 1)
+            logits = self._forward(cond)
+            nxt = self._sample(logits[:, -1, :], temperature, top_k)
             idx = torch.cat([idx, nxt], dim=1)
         return idx
+
+    @staticmethod
+    def _sample(logits: torch.Tensor, temperature: float, top_k: Optional[int]) -> torch.Tensor:
+        """Next token (B, 1) from last-position logits (B, V): temperature,
+        top-k masking, argmax for top_k == 1 else multinomial sampling
+        (``cutile_gpt/models/gpt.py:207-226``)."""
+        logits = logits.float() / temperature
+        if top_k is not None:
+            k = min(top_k, logits.shape[-1])
+            kth = torch.topk(logits, k, dim=-1).values[:, -1:]
+            logits = logits.masked_fill(logits < kth, float("-inf"))
+        if top_k == 1:
+            return logits.argmax(-1, keepdim=True)
+        probs = torch.softmax(logits, dim=-1)
+        return torch.multinomial(probs, 1)
 
     # ------------------------------------------------------------------ loaders
 

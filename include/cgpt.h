@@ -82,12 +82,15 @@ int cgpt_add_layernorm(const void* x, const void* delta, void* x_out,
  * fp32 MFMA); accumulation is fp32; bias (bias_dtype) is added in fp32; C is
  * written as out_dtype.  Requires K % 8 == 0 (bf16) or K % 4 == 0 (fp32), lda /
  * ldw multiples of 8 (bf16) or 4 (fp32) elements and 16-byte aligned A, W and bias.
- * `tile` selects a tile configuration (CGPT_TILE_AUTO = library heuristic).
+ * `tile` selects a tile configuration: CGPT_TILE_AUTO = library heuristic (the
+ * skinny kernel when M <= 64); CGPT_TILE_SKINNY = the weight-streaming kernel
+ * for M <= 64 rows (decode steps: one row per sequence), CGPT_ESHAPE above.
  * Replaces cutile_linear / cutile_linear_bias, cutile_gpt/kernels/linear.py:112-222
  * (kernels :37-109); CGPT_EPI_BIAS_GELU also absorbs cutile_gelu at
  * cutile_gpt/models/gpt.py:167.
  */
 #define CGPT_TILE_AUTO (-1)
+#define CGPT_TILE_SKINNY (-2)
 int cgpt_gemm(const void* a, const void* w, const void* bias, void* c,
               int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldc,
               int in_dtype, int bias_dtype, int out_dtype, int epilogue, int tile,
@@ -131,6 +134,64 @@ int cgpt_embedding(const int64_t* idx, const void* wte, const void* wpe, void* o
                    int64_t n_tokens, int64_t T, int64_t D, int64_t vocab,
                    int64_t pos0, int64_t n_pos, int w_dtype, int out_dtype,
                    int* err_flag, void* stream);
+
+/*
+ * Embedding of one decode step: out[i, :] = wte[idx[i], :] + wpe[pos_base + *pos_dev, :]
+ * for i < n_tokens (one token per sequence, all at the same position), with the
+ * position read from device memory (an int) when the kernel runs, so a
+ * captured step replays unchanged.  Clamping and err_flag as cgpt_embedding.
+ * No reference counterpart: the reference re-embeds the whole prefix every
+ * step (generate, cutile_gpt/models/gpt.py:185-229 calling forward :109-113).
+ */
+int cgpt_embedding_at(const int64_t* idx, const void* wte, const void* wpe, void* out,
+                      int64_t n_tokens, int64_t D, int64_t vocab, int64_t pos_base,
+                      const int* pos_dev, int64_t n_pos, int w_dtype, int out_dtype,
+                      int* err_flag, void* stream);
+
+/*
+ * Single-query attention over a KV cache, one decode step for B sequences x H
+ * heads.  Cache element (b, h, t, d) lives at base + b*c_sb + h*c_sh + t*c_st + d
+ * (k_cache and v_cache share the strides; 16-byte aligned rows).  With
+ * pos = pos_base + (*pos_dev if pos_dev else 0): writes k_new / v_new (the
+ * step's key and value, (b, h, d) at base + b*sb + h*sh + d) into cache row
+ * pos, then o = softmax(q K[0..pos]^T * scale) V[0..pos] — the causal row of
+ * position pos.  P is rounded to `dtype` before the P*V product, as in
+ * cgpt_attention_fwd.  head_dim divides 256 and is a multiple of 8 (bf16) / 4
+ * (fp32); t_max <= 16384.  A device pos outside [0, t_max) is clamped and sets
+ * *err_flag.  Replaces the per-token full recompute of cutile_causal_attention
+ * inside generate (cutile_gpt/models/gpt.py:185-229, attention.py:119-175).
+ */
+int cgpt_attention_decode(const void* q, const void* k_new, const void* v_new,
+                          void* k_cache, void* v_cache, void* o, int64_t B, int64_t H,
+                          int64_t head_dim, int64_t t_max, int64_t pos_base,
+                          const int* pos_dev, int64_t q_sb, int64_t q_sh,
+                          int64_t kn_sb, int64_t kn_sh, int64_t vn_sb, int64_t vn_sh,
+                          int64_t c_sb, int64_t c_sh, int64_t c_st, int64_t o_sb,
+                          int64_t o_sh, float scale, int dtype, int* err_flag,
+                          void* stream);
+
+/*
+ * Copy T positions of keys and values ((b, h, t, d) at base + b*sb + h*sh + t*st
+ * + d, e.g. strided views into a fused QKV buffer) into cache rows
+ * pos0 .. pos0+T-1 (cache strides as cgpt_attention_decode; pos0 + T <= t_max).
+ * Fills the cache after a prefill.  No reference counterpart (the reference
+ * keeps no cache, cutile_gpt/models/gpt.py:185-229).
+ */
+int cgpt_kv_store(const void* k, const void* v, void* k_cache, void* v_cache, int64_t B,
+                  int64_t H, int64_t T, int64_t head_dim, int64_t pos0, int64_t t_max,
+                  int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t v_sb, int64_t v_sh,
+                  int64_t v_st, int64_t c_sb, int64_t c_sh, int64_t c_st, int dtype,
+                  void* stream);
+
+/*
+ * Greedy token per row: ids[r] = argmax_c x[r * ld + c] (the first maximum;
+ * NaN entries are skipped), also stored at hist[r * hist_ld + *step_dev] when
+ * hist is not NULL (step_dev NULL: column 0).  Replaces the top_k = 1 case of
+ * generate's sampling, cutile_gpt/models/gpt.py:207-226.
+ */
+int cgpt_argmax(const void* x, int64_t rows, int64_t cols, int64_t ld, int dtype,
+                int64_t* ids, int64_t* hist, int64_t hist_ld, const int* step_dev,
+                void* stream);
 
 #ifdef __cplusplus
 }

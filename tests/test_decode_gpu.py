@@ -1,0 +1,320 @@
+"""KV-cache decoding on the GPU: the skinny GEMM, decode attention, cache fill,
+device-position embedding and argmax kernels against the CPU oracle, and the
+decode loop against the full-recompute forward and the oracle's greedy stream.
+
+Tolerances: fp32 max |error| <= 1e-3 (the benchmark's fp32 logit bound; kernel
+level checks use tighter ones where noted); bf16 outputs within 3e-2 or a few
+bf16 ulps of the exact (fp64) result.
+"""
+
+import math
+
+import pytest
+import torch
+
+from cutilegpt_amd import CutileGPT, GPTConfig, _lib
+from cutilegpt_amd.decode import DecodeSession, KVCache
+from oracle import gpt_ref as R
+
+pytestmark = pytest.mark.gpu
+DT = {torch.float32: _lib.CGPT_F32, torch.bfloat16: _lib.CGPT_BF16}
+
+
+def stream(dev):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+# ------------------------------------------------------------------ skinny GEMM
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("M,N,K", [(1, 16, 64), (5, 50, 72), (16, 1600, 1600), (17, 96, 256),
+                                   (32, 4800, 1600), (33, 70, 520), (64, 200, 6400),
+                                   (32, 50257, 64)])
+@pytest.mark.parametrize("epi", [_lib.EPI_NONE, _lib.EPI_BIAS, _lib.EPI_BIAS_GELU])
+def test_skinny_gemm_vs_fp64(gpu, dtype, M, N, K, epi):
+    g = torch.Generator().manual_seed(M * 7919 + N * 31 + K)
+    a = torch.randn(M, K, generator=g).to(dtype)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(dtype)
+    b = torch.randn(N, generator=g).to(dtype)
+    ref = a.double() @ w.double().t()
+    if epi != _lib.EPI_NONE:
+        ref = ref + b.double()
+    if epi == _lib.EPI_BIAS_GELU:
+        ref = R.gelu_tanh(ref)
+    for out_dtype in (torch.float32, dtype):
+        c = torch.full((M, N), float("nan"), dtype=out_dtype, device=gpu)
+        lib = _lib.load()
+        ad, wd, bd = a.to(gpu), w.to(gpu), b.to(gpu)
+        _lib.check(lib.cgpt_gemm(ad.data_ptr(), wd.data_ptr(), bd.data_ptr(), c.data_ptr(), M, N, K,
+                                 K, K, N, DT[dtype], DT[dtype], DT[out_dtype], epi,
+                                 _lib.TILE_SKINNY, stream(gpu)), "skinny")
+        torch.cuda.synchronize()
+        err = (c.double().cpu() - ref).abs()
+        scale = ref.abs().max().item() + 1.0
+        # fp32: accumulation-order noise only.  bf16 inputs are exact in the
+        # reference; a bf16 output adds half an ulp (2^-9 relative).
+        tol = 1e-4 * scale if out_dtype == torch.float32 else 4e-3 * scale
+        assert torch.isfinite(c).all()
+        assert err.max().item() <= tol, (M, N, K, epi, out_dtype, err.max().item())
+
+
+def test_skinny_auto_tile_and_limits(gpu):
+    lib = _lib.load()
+    a = torch.randn(65, 64, device=gpu).bfloat16()
+    w = torch.randn(32, 64, device=gpu).bfloat16()
+    c = torch.empty(65, 32, device=gpu, dtype=torch.float32)
+    st = lib.cgpt_gemm(a.data_ptr(), w.data_ptr(), None, c.data_ptr(), 65, 32, 64, 64, 64, 32,
+                       _lib.CGPT_BF16, _lib.CGPT_BF16, _lib.CGPT_F32, _lib.EPI_NONE,
+                       _lib.TILE_SKINNY, stream(gpu))
+    assert st == -3  # CGPT_ESHAPE: the skinny kernel takes at most 64 rows
+    # TILE_AUTO picks the skinny kernel at M <= 64 and must match it exactly.
+    c1 = torch.empty(40, 32, device=gpu)
+    c2 = torch.empty(40, 32, device=gpu)
+    for c_, tile in ((c1, _lib.TILE_AUTO), (c2, _lib.TILE_SKINNY)):
+        _lib.check(lib.cgpt_gemm(a.data_ptr(), w.data_ptr(), None, c_.data_ptr(), 40, 32, 64, 64,
+                                 64, 32, _lib.CGPT_BF16, _lib.CGPT_BF16, _lib.CGPT_F32,
+                                 _lib.EPI_NONE, tile, stream(gpu)), "gemm")
+    torch.cuda.synchronize()
+    assert torch.equal(c1, c2)
+
+
+# ------------------------------------------------------------- decode attention
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("hd", [16, 64, 128])
+@pytest.mark.parametrize("pos", [0, 17, 39])
+def test_attention_decode_vs_oracle(gpu, dtype, hd, pos):
+    B, H, t_max = 3, 2, 40
+    g = torch.Generator().manual_seed(pos * 131 + hd)
+    cache_k = torch.randn(B, H, t_max, hd, generator=g).to(dtype)
+    cache_v = torch.randn(B, H, t_max, hd, generator=g).to(dtype)
+    q = torch.randn(B, H, hd, generator=g).to(dtype)
+    kn = torch.randn(B, H, hd, generator=g).to(dtype)
+    vn = torch.randn(B, H, hd, generator=g).to(dtype)
+    kc, vc = cache_k.to(gpu), cache_v.to(gpu)
+    qd, knd, vnd = q.to(gpu), kn.to(gpu), vn.to(gpu)
+    o = torch.empty(B, H, hd, dtype=dtype, device=gpu)
+    err = torch.zeros(1, dtype=torch.int32, device=gpu)
+    # Device position: pos_base 5 + *pos_dev.
+    pdev = torch.tensor([pos - 5], dtype=torch.int32, device=gpu)
+    lib = _lib.load()
+    cs = kc.stride()
+    _lib.check(lib.cgpt_attention_decode(qd.data_ptr(), knd.data_ptr(), vnd.data_ptr(),
+                                         kc.data_ptr(), vc.data_ptr(), o.data_ptr(), B, H, hd,
+                                         t_max, 5, pdev.data_ptr(), H * hd, hd, H * hd, hd,
+                                         H * hd, hd, cs[0], cs[1], cs[2], H * hd, hd,
+                                         1.0 / math.sqrt(hd), DT[dtype], err.data_ptr(),
+                                         stream(gpu)), "attention_decode")
+    torch.cuda.synchronize()
+    assert err.item() == 0
+    # The step's key/value were appended at pos; every other row is untouched.
+    exp_k, exp_v = cache_k.clone(), cache_v.clone()
+    exp_k[:, :, pos], exp_v[:, :, pos] = kn, vn
+    assert torch.equal(kc.cpu(), exp_k) and torch.equal(vc.cpu(), exp_v)
+    ref = R.causal_attention(q.double().unsqueeze(2), exp_k[:, :, :pos + 1].double(),
+                             exp_v[:, :, :pos + 1].double(),
+                             p_dtype=None if dtype == torch.float32 else torch.bfloat16)
+    e = (o.double().cpu() - ref.squeeze(2)).abs().max().item()
+    assert e <= (2e-5 if dtype == torch.float32 else 2e-2), e
+
+
+def test_attention_decode_single_key_is_value(gpu):
+    # pos 0: the only visible key is the appended one, so o == v_new exactly.
+    B, H, hd, t_max = 2, 3, 64, 8
+    kc = torch.randn(B, H, t_max, hd, device=gpu)
+    vc = torch.randn(B, H, t_max, hd, device=gpu)
+    q, kn, vn = (torch.randn(B, H, hd, device=gpu) for _ in range(3))
+    o = torch.empty(B, H, hd, device=gpu)
+    cs = kc.stride()
+    lib = _lib.load()
+    _lib.check(lib.cgpt_attention_decode(q.data_ptr(), kn.data_ptr(), vn.data_ptr(), kc.data_ptr(),
+                                         vc.data_ptr(), o.data_ptr(), B, H, hd, t_max, 0, None,
+                                         H * hd, hd, H * hd, hd, H * hd, hd, cs[0], cs[1], cs[2],
+                                         H * hd, hd, 0.125, _lib.CGPT_F32, None, stream(gpu)), "dec")
+    torch.cuda.synchronize()
+    assert torch.allclose(o, vn, rtol=0, atol=1e-6)
+
+
+def test_attention_decode_rejects_bad_args(gpu):
+    lib = _lib.load()
+    t = torch.zeros(4096, device=gpu)
+    p = t.data_ptr()
+    # host position outside the cache, head_dim not dividing 256, misaligned cache rows
+    assert lib.cgpt_attention_decode(p, p, p, p, p, p, 1, 1, 64, 8, 8, None, 64, 64, 64, 64, 64,
+                                     64, 512, 512, 64, 64, 64, 1.0, _lib.CGPT_F32, None, 0) == -1
+    assert lib.cgpt_attention_decode(p, p, p, p, p, p, 1, 1, 48, 8, 0, None, 48, 48, 48, 48, 48,
+                                      48, 384, 384, 48, 48, 48, 1.0, _lib.CGPT_F32, None, 0) == -3
+    assert lib.cgpt_attention_decode(p, p, p, p, p, p, 1, 1, 64, 8, 0, None, 64, 64, 64, 64, 64,
+                                      64, 512, 512, 66, 64, 64, 1.0, _lib.CGPT_F32, None, 0) == -1
+
+
+def test_attention_decode_clamps_device_pos(gpu):
+    B, H, hd, t_max = 1, 1, 64, 4
+    kc = torch.zeros(B, H, t_max, hd, device=gpu)
+    vc = torch.zeros(B, H, t_max, hd, device=gpu)
+    q, kn, vn = (torch.randn(B, H, hd, device=gpu) for _ in range(3))
+    o = torch.empty(B, H, hd, device=gpu)
+    err = torch.zeros(1, dtype=torch.int32, device=gpu)
+    pdev = torch.tensor([9], dtype=torch.int32, device=gpu)  # 9 >= t_max
+    cs = kc.stride()
+    lib = _lib.load()
+    _lib.check(lib.cgpt_attention_decode(q.data_ptr(), kn.data_ptr(), vn.data_ptr(), kc.data_ptr(),
+                                         vc.data_ptr(), o.data_ptr(), B, H, hd, t_max, 0,
+                                         pdev.data_ptr(), hd, hd, hd, hd, hd, hd, cs[0], cs[1],
+                                         cs[2], hd, hd, 0.125, _lib.CGPT_F32, err.data_ptr(),
+                                         stream(gpu)), "dec")
+    torch.cuda.synchronize()
+    assert err.item() == 1
+    assert torch.equal(kc[0, 0, t_max - 1], kn[0, 0])  # clamped into the last row
+
+
+# ------------------------------------------------------- cache fill, argmax, embedding
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_kv_store_copies_strided_qkv(gpu, dtype):
+    B, T, H, hd, t_max, pos0 = 2, 7, 3, 32, 12, 4
+    D = H * hd
+    qkv = torch.randn(B, T, 3 * D, device=gpu).to(dtype)
+    kc = torch.zeros(B, H, t_max, hd, dtype=dtype, device=gpu)
+    vc = torch.zeros(B, H, t_max, hd, dtype=dtype, device=gpu)
+    esz = qkv.element_size()
+    cs = kc.stride()
+    lib = _lib.load()
+    _lib.check(lib.cgpt_kv_store(qkv.data_ptr() + D * esz, qkv.data_ptr() + 2 * D * esz,
+                                 kc.data_ptr(), vc.data_ptr(), B, H, T, hd, pos0, t_max,
+                                 T * 3 * D, hd, 3 * D, T * 3 * D, hd, 3 * D, cs[0], cs[1], cs[2],
+                                 DT[dtype], stream(gpu)), "kv_store")
+    torch.cuda.synchronize()
+    k = qkv[:, :, D:2 * D].view(B, T, H, hd).transpose(1, 2)
+    v = qkv[:, :, 2 * D:].view(B, T, H, hd).transpose(1, 2)
+    assert torch.equal(kc[:, :, pos0:pos0 + T], k) and torch.equal(vc[:, :, pos0:pos0 + T], v)
+    assert (kc[:, :, :pos0] == 0).all() and (kc[:, :, pos0 + T:] == 0).all()
+    assert lib.cgpt_kv_store(qkv.data_ptr(), qkv.data_ptr(), kc.data_ptr(), vc.data_ptr(), B, H,
+                             T, hd, 6, t_max, T * 3 * D, hd, 3 * D, T * 3 * D, hd, 3 * D, cs[0],
+                             cs[1], cs[2], DT[dtype], 0) == -3  # 6 + 7 > 12
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_argmax_first_maximum_and_history(gpu, dtype):
+    rows, cols = 5, 50257
+    x = torch.randn(rows, cols, device=gpu).to(dtype)
+    x[1, 100] = x[1, 9000] = 1e4  # tie: the first index wins
+    x[2, :] = float("-inf")
+    x[2, 7] = 0.0
+    x[3, 3] = float("nan")        # NaN entries are skipped
+    x[3, 11] = 1e4
+    ids = torch.full((rows,), -1, dtype=torch.int64, device=gpu)
+    hist = torch.full((rows, 4), -1, dtype=torch.int64, device=gpu)
+    step = torch.tensor([2], dtype=torch.int32, device=gpu)
+    lib = _lib.load()
+    _lib.check(lib.cgpt_argmax(x.data_ptr(), rows, cols, cols, DT[dtype], ids.data_ptr(),
+                               hist.data_ptr(), 4, step.data_ptr(), stream(gpu)), "argmax")
+    torch.cuda.synchronize()
+    xc = x.float().cpu()
+    xc[3, 3] = -float("inf")
+    exp = xc.argmax(-1)
+    assert ids.cpu().tolist() == exp.tolist()
+    assert ids[1].item() == 100 and ids[2].item() == 7 and ids[3].item() == 11
+    assert hist[:, 2].cpu().tolist() == exp.tolist()
+    assert (hist[:, [0, 1, 3]] == -1).all()
+
+
+def test_embedding_at_device_position(gpu):
+    V, D, P = 97, 64, 32
+    wte = torch.randn(V, D, device=gpu).bfloat16()
+    wpe = torch.randn(P, D, device=gpu).bfloat16()
+    idx = torch.tensor([3, 96, 0, 50], dtype=torch.int64, device=gpu)
+    out = torch.empty(4, D, device=gpu)
+    pdev = torch.tensor([6], dtype=torch.int32, device=gpu)
+    err = torch.zeros(1, dtype=torch.int32, device=gpu)
+    lib = _lib.load()
+    _lib.check(lib.cgpt_embedding_at(idx.data_ptr(), wte.data_ptr(), wpe.data_ptr(),
+                                     out.data_ptr(), 4, D, V, 10, pdev.data_ptr(), P,
+                                     _lib.CGPT_BF16, _lib.CGPT_F32, err.data_ptr(), stream(gpu)),
+               "embedding_at")
+    torch.cuda.synchronize()
+    exp = wte[idx].float() + wpe[16].float()
+    assert torch.equal(out, exp) and err.item() == 0
+    assert lib.cgpt_embedding_at(idx.data_ptr(), wte.data_ptr(), wpe.data_ptr(), out.data_ptr(),
+                                 4, D, V, 0, None, P, _lib.CGPT_BF16, _lib.CGPT_F32, None, 0) == -1
+
+
+# ------------------------------------------------------------------ model level
+
+def small_model(dtype, n_layer=2, n_head=4, n_embd=128, seed=3):
+    cfg = GPTConfig(n_layer=n_layer, n_head=n_head, n_embd=n_embd, block_size=1024)
+    w = R.init_weights(n_layer, n_head, n_embd, seed=seed)
+    m = CutileGPT(cfg, dtype=dtype, seed=0)
+    m.load_weights(w)
+    return m, w, cfg
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decode_logits_match_full_forward(gpu, dtype):
+    """Each cached step's logits equal the full forward's at that position."""
+    m, _, cfg = small_model(dtype)
+    B, T0, n = 4, 9, 12
+    idx = torch.randint(0, cfg.vocab_size, (B, T0), generator=torch.Generator().manual_seed(5)).to(gpu)
+    sess = DecodeSession(m, B, T0, n)
+    sess.prefill(idx)
+    seen = [sess.logits.float().clone()]
+    sess.greedy_first()
+    for _ in range(n - 1):
+        sess.greedy_step()
+        seen.append(sess.logits.float().clone())
+    torch.cuda.synchronize()
+    seq = torch.cat([idx, sess.hist], dim=1)
+    full, _ = m.forward(seq)
+    tol = 1e-3 if dtype == torch.float32 else 3e-2
+    for s, lg in enumerate(seen):
+        ref = full[:, T0 - 1 + s, :].float()
+        e = (lg - ref).abs().max().item()
+        assert e <= tol, (s, e)
+        assert torch.equal(sess.hist[:, s], lg.argmax(-1))
+    assert sess.err.item() == 0 and sess.step.item() == n - 1
+
+
+def test_greedy_graph_replay_equals_eager(gpu):
+    """Replaying the captured step gives exactly the eager tokens (every
+    replay is checked through the history it writes)."""
+    m, _, cfg = small_model(torch.bfloat16)
+    B, T0, n = 8, 16, 24
+    idx = torch.randint(0, cfg.vocab_size, (B, T0), generator=torch.Generator().manual_seed(9)).to(gpu)
+    eager = m.generate(idx, n, top_k=1, use_graph=False)
+    graph = m.generate(idx, n, top_k=1, use_graph=True)
+    assert torch.equal(eager, graph)
+    again = m.generate(idx, n, top_k=1, use_graph=True)
+    assert torch.equal(eager, again)
+
+
+def test_greedy_stream_fp32_vs_oracle(gpu):
+    """fp32 KV-cache greedy stream == the oracle's full-recompute greedy stream."""
+    m, w, cfg = small_model(torch.float32, n_layer=2, n_head=2, n_embd=64, seed=11)
+    B, T0, n = 3, 5, 10
+    idx = torch.randint(0, cfg.vocab_size, (B, T0), generator=torch.Generator().manual_seed(2))
+    ref = R.generate(w, idx, cfg.n_head, n)
+    out = m.generate(idx.to(gpu), n, top_k=1)
+    assert torch.equal(out.cpu(), ref)
+    out_nc = m.generate(idx.to(gpu), n, top_k=1, use_cache=False)
+    assert torch.equal(out_nc.cpu(), ref)
+
+
+def test_sampled_generate_with_cache_is_reproducible(gpu):
+    m, _, cfg = small_model(torch.bfloat16)
+    idx = torch.randint(0, cfg.vocab_size, (2, 6), generator=torch.Generator().manual_seed(4)).to(gpu)
+    torch.manual_seed(123)
+    a = m.generate(idx, 7, temperature=0.8, top_k=20)
+    torch.manual_seed(123)
+    b = m.generate(idx, 7, temperature=0.8, top_k=20)
+    assert a.shape == (2, 13) and torch.equal(a, b)
+    assert ((a >= 0) & (a < cfg.vocab_size)).all()
+
+
+def test_decode_session_limits(gpu):
+    m, _, cfg = small_model(torch.bfloat16)
+    with pytest.raises(ValueError):
+        DecodeSession(m, 2, 1000, 25)   # past block_size
+    with pytest.raises(ValueError):
+        DecodeSession(m, 65, 4, 4)      # more sequences than the skinny kernel takes
+    c = KVCache(2, 3, 4, 10, 16, torch.bfloat16, gpu)
+    assert c.strides() == (4 * 10 * 16, 10 * 16, 16)
