@@ -1,6 +1,6 @@
 """Prefill throughput of the GPT-2 forward hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload gpt2|medium]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload gpt2|medium|xl-decode]
 
 Workload (default): GPT-2 124M architecture (12 layers, 12 heads, d 768, MLP 3072,
 vocab 50257), bf16 random-init weights N(0, 0.02) written as an HF GPT-2
@@ -15,6 +15,15 @@ steps.  ``cpu_baseline`` is the CPU oracle's fp32 forward of the same model
 (a minGPT-architecture PyTorch forward) on the host cores, over a bounded
 sample.  ``breakdown`` comes from one extra, separately timed forward with
 events around every launch.
+
+``--workload xl-decode``: KV-cache greedy decoding of GPT-2 XL (48 layers, 25
+heads, d 1600), bf16 N(0, 0.02) weights generated on the device, batch 32,
+prompt 128, 128 new tokens.  A step = one captured decode step (all 32
+sequences advance one token), replayed from a HIP graph; ``value`` is steady
+decode tok/s (32 / step time), ``e2e`` the whole ``generate`` call (prefill +
+128 tokens).  ``roofline`` is HBM: the step's algorithmic bytes (every weight
+once + the KV cache rows read) over the step time, and the LM-head skinny GEMM
+alone.
 """
 
 from __future__ import annotations
@@ -59,7 +68,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="gpt2", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="gpt2", choices=sorted(WORKLOADS) + ["xl-decode"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seqs", type=int, default=2,
                     help="sequences (of seq_len tokens) per timed CPU-baseline forward")
@@ -72,6 +81,10 @@ def main():
         print("bench.py: this build measures one GPU only (every box has a single MI355X); "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+
+    if args.workload == "xl-decode":
+        bench_xl_decode(args)
+        return
 
     import torch
     from cutilegpt_amd import CutileGPT, GPTConfig
@@ -209,6 +222,130 @@ def main():
         "forward_tflops": round((gemm_f + head_f + attn_f) / (ms_per_step * 1e-3) / 1e12, 1),
         "breakdown": breakdown,
         "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def bench_xl_decode(args):
+    """GPT-2 XL KV-cache greedy decode, b32, prompt 128 + 128 new tokens."""
+    import statistics
+
+    import torch
+    from cutilegpt_amd import CutileGPT, GPTConfig, _lib
+    from cutilegpt_amd.decode import DecodeSession
+
+    L, H, D, B, T0, NEW, V = 48, 25, 1600, 32, 128, 128, 50257
+    hd = D // H
+    cfg = GPTConfig(vocab_size=V, block_size=1024, n_layer=L, n_head=H, n_embd=D)
+    dev = torch.device("cuda:0")
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(0)
+    rn = lambda *s: (torch.randn(*s, generator=g, device=dev) * 0.02).to(bf)
+    ones = lambda n: torch.ones(n, dtype=bf, device=dev)
+    zeros = lambda n: torch.zeros(n, dtype=bf, device=dev)
+    w = {"wte": rn(V, D), "wpe": rn(1024, D), "ln_f.weight": ones(D), "ln_f.bias": zeros(D)}
+    for i in range(L):
+        p = f"h.{i}."
+        w[p + "ln_1.weight"], w[p + "ln_1.bias"] = ones(D), zeros(D)
+        w[p + "attn.c_attn.weight"], w[p + "attn.c_attn.bias"] = rn(3 * D, D), zeros(3 * D)
+        w[p + "attn.c_proj.weight"], w[p + "attn.c_proj.bias"] = rn(D, D), zeros(D)
+        w[p + "ln_2.weight"], w[p + "ln_2.bias"] = ones(D), zeros(D)
+        w[p + "mlp.c_fc.weight"], w[p + "mlp.c_fc.bias"] = rn(4 * D, D), zeros(4 * D)
+        w[p + "mlp.c_proj.weight"], w[p + "mlp.c_proj.bias"] = rn(D, 4 * D), zeros(D)
+    model = CutileGPT(cfg, dtype=bf, init_weights=False)
+    model.load_weights(w)
+    del w
+    ids = torch.randint(0, V, (B, T0), generator=torch.Generator().manual_seed(1)).to(dev)
+    print(f"[bench] workload gpt2-xl decode b{B} {T0}+{NEW}: warmup {args.warmup}, "
+          f"steps {args.steps}", file=sys.stderr, flush=True)
+
+    # End to end: generate() = prefill + 128 greedy tokens (graph replay).
+    for _ in range(max(1, args.warmup // 5)):
+        model.generate(ids, NEW, top_k=1)
+    torch.cuda.synchronize()
+    e2e = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        out = model.generate(ids, NEW, top_k=1)
+        torch.cuda.synchronize()
+        e2e.append(time.perf_counter() - t0)
+    e2e_s = statistics.median(e2e)
+
+    # Steady decode: one captured step replayed; the step counter is reset so
+    # every replay sees the same positions (T0 .. T0+K-1 cycle).
+    sess = DecodeSession(model, B, T0, NEW)
+    sess.prefill(ids)
+    sess.greedy_first()
+    sess.greedy_step()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.graph(graph, stream=side):
+        sess.greedy_step()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    k = min(args.steps, NEW - 2)
+    for _ in range(args.warmup):
+        sess.step.fill_(1)
+        graph.replay()
+    sess.step.fill_(1)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(k):
+        graph.replay()
+    torch.cuda.synchronize()
+    step_s = (time.perf_counter() - t0) / k
+    mean_ctx = T0 + 1 + (k - 1) / 2.0 + 1  # keys visible per step, averaged
+
+    # LM-head skinny GEMM alone (the single largest launch of a step).
+    lib = _lib.load()
+    st = torch.cuda.current_stream(dev)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    head_w = model.weights["lm_head.weight"]
+    call = lambda: _lib.check(lib.cgpt_gemm_skinny(sess.h.data_ptr(), head_w.data_ptr(), None,
+                                                   sess.logits.data_ptr(), B, V, D, D, D, V,
+                                                   _lib.CGPT_BF16, _lib.CGPT_BF16, _lib.CGPT_F32,
+                                                   _lib.EPI_NONE, sess.ws.data_ptr(), sess.ws_bytes,
+                                                   sess.counters.data_ptr(), sess.counters.numel(),
+                                                   st.cuda_stream), "head")
+    for _ in range(3):
+        call()
+    ev0.record(st)
+    for _ in range(20):
+        call()
+    ev1.record(st)
+    torch.cuda.synchronize()
+    head_ms = ev0.elapsed_time(ev1) / 20
+    head_bytes = V * D * 2 + B * D * 2 + B * V * 4
+
+    weight_bytes = L * 12 * D * D * 2 + L * (3 * D + D + 4 * D + D + 4 * D) * 2 + V * D * 2
+    kv_bytes = L * 2 * B * H * mean_ctx * hd * 2
+    step_bytes = weight_bytes + kv_bytes
+    line = {
+        "metric": "decode tok/s (GPT-2 XL, b32, 128+128 greedy, bf16)",
+        "value": round(B / step_s, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": k,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_s * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random N(0,0.02) bf16 weights generated on device, uniform ids)",
+        "config": {"workload": "gpt2-xl decode b32 128+128 greedy", "n_layer": L, "n_head": H,
+                   "n_embd": D, "vocab_size": V, "batch": B, "prompt": T0, "new_tokens": NEW,
+                   "parallelism": "single GPU"},
+        "e2e": {"generate_s": round(e2e_s, 4), "tok_s": round(B * NEW / e2e_s, 1),
+                "what": "generate(top_k=1): prefill 32x128 + 128 tokens, graph replay"},
+        "roofline": {"bound": "hbm", "kernel": "decode step (skinny GEMMs + decode attention)",
+                     "achieved": round(step_bytes / step_s / 1e9, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(step_bytes / step_s / 1e9 / PEAK_HBM_GBS, 4),
+                     "traffic": None, "bytes_per_step": int(step_bytes),
+                     "lm_head_skinny": {"avg_launch_ms": round(head_ms, 4),
+                                        "achieved_GBs": round(head_bytes / head_ms / 1e6, 1),
+                                        "frac": round(head_bytes / head_ms / 1e6 / PEAK_HBM_GBS, 4)}},
+        "cpu_baseline": None,
     }
     print(json.dumps(line), flush=True)
 

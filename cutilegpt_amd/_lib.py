@@ -39,6 +39,9 @@ SIGNATURES = {
     "cgpt_add_layernorm": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _F, _I, _I, _I, _I, _P]),
     "cgpt_gemm": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _I, _I, _I, _P]),
     "cgpt_gemm_num_tiles": (_I, []),
+    "cgpt_gemm_skinny": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _I, _I,
+                              _P, _I64, _P, _I64, _P]),
+    "cgpt_gemm_skinny_workspace": (_I, [_I64, _I64, _I64, _I, _P, _P]),
     "cgpt_attention_fwd": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
                                 _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
                                 _I64, _I64, _I64, _F, _I, _I, _P]),

@@ -4,13 +4,11 @@
 //  * gemm_skinny_kernel — C[M,N] = epi(A W^T + bias) for M <= 64 (one row per
 //    sequence in the batch).  Decode GEMMs are weight-streaming: every weight
 //    byte is read once per step, so the kernel is built around HBM traffic,
-//    not MFMA reuse.  Block = 8 waves sharing one 16-column slice of W; each
-//    wave streams a contiguous K range of those 16 rows straight from global
-//    memory into registers in MFMA fragment order (lane l: row l % 16, k chunk
-//    l / 16 — the same 16-byte fragments the prefill GEMM reads from LDS), with
-//    8 slabs of loads in flight, and multiplies them against the (L2-resident)
-//    activation rows.  The 8 partial 16 x M accumulators are summed through
-//    LDS, then bias / GELU / store.  No workspace, deterministic.
+//    not MFMA reuse: W rows go straight from global memory into MFMA fragments
+//    (no LDS staging), several full cache lines per lane in flight, against
+//    the (L2-resident) activation rows; K is split across the waves of a block
+//    and, with a caller workspace, across blocks (deterministic fix-up by the
+//    last block of each column slice).
 //  * attn_decode_kernel — one block per (batch, head): appends the step's key
 //    and value to the cache at position pos, then softmax(q K^T * scale) V
 //    over cache rows 0..pos.  pos = pos_base + *pos_dev, read on the device so
@@ -27,80 +25,206 @@ namespace cgpt {
 
 // --------------------------------------------------------------- skinny GEMM
 
-constexpr int kSkWaves = 8;
-constexpr int kSkUnroll = 8;
+constexpr int kSkWaves = 8;      // waves per block, splitting the block's K range
+constexpr int kSkNT = 4;         // 16-column n-tiles per block (64 columns)
+constexpr int kSkU = 2;          // double slabs in flight per wave
+constexpr int kSkTargetBlocks = 512;
+constexpr int kSkMaxSplit = 16;  // K chunks per column slice at most
+constexpr int kCpolSc1 = 16;     // buffer cache-policy bits: sc1 (agent scope)
 
 __device__ __forceinline__ float bias_value(const void* bias, bool bf16, int n) {
   return bf16 ? bf16_to_f32(static_cast<const bf16_t*>(bias)[n]) : static_cast<const float*>(bias)[n];
 }
 
+// Work split shared by the launcher and the workspace query: 64-column slices
+// x `split` K chunks.
+struct SkinnyPlan {
+  int slices, dslabs, split, mt;
+  int64_t ws_floats;  // per-block partial tiles, all blocks
+};
+
+static SkinnyPlan skinny_plan(int M, int N, int K, int elem_bytes, bool have_ws) {
+  SkinnyPlan p;
+  const int kd = 8 * (16 / elem_bytes);  // k per double slab
+  p.mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+  p.slices = (N + 16 * kSkNT - 1) / (16 * kSkNT);
+  p.dslabs = (K + kd - 1) / kd;
+  int split = 1;
+  if (have_ws) {
+    // About kSkTargetBlocks blocks, but every wave of a block keeps at least
+    // one double slab and at most kSkMaxSplit chunks per slice.
+    split = (kSkTargetBlocks + p.slices - 1) / p.slices;
+    int cap = p.dslabs / kSkWaves;
+    cap = cap < kSkMaxSplit ? cap : kSkMaxSplit;
+    split = split < cap ? split : cap;
+    split = split > 1 ? split : 1;
+  }
+  p.split = split;
+  p.ws_floats = split > 1 ? static_cast<int64_t>(p.slices) * split * p.mt * kSkNT * 64 * 4 : 0;
+  return p;
+}
+
+// C[M,N] = epi(A W^T + bias) for M <= 16 * MT.  Block = 64 output columns
+// (4 n-tiles) x one K chunk; its 8 waves split the chunk and stream W rows
+// straight into MFMA fragments.  A "double slab" covers 2 * 4 * EPC k: lane
+// group g loads 32 contiguous bytes of each row (k = 2g EPC .. 2g EPC + 2 EPC),
+// so the 4 groups of a row read one full 128-byte line per load pair; the two
+// 16-byte halves feed two MFMAs (any consistent assignment of k to MFMA slots
+// gives the same sums, and A uses the same one).  Partial tiles are summed
+// across waves through LDS in wave order; with split > 1 each block writes its
+// sum to the workspace and the last block of a slice (counted on a device
+// atomic) adds the split partials in chunk order, applies the epilogue and
+// resets the counter — deterministic, and no clearing is needed between calls.
 template <typename TIn, int MT, int EPI, typename TOut>
 __global__ __launch_bounds__(64 * kSkWaves) void gemm_skinny_kernel(
     const TIn* __restrict__ A, const TIn* __restrict__ W, const void* __restrict__ bias,
     bool bias_bf16, TOut* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldw,
-    int64_t ldc, bool vec_store) {
-  constexpr int EPC = 16 / sizeof(TIn);  // elements per 16-byte fragment
-  constexpr int KS = 4 * EPC;            // k per slab (4 lane groups)
-  constexpr int U = kSkUnroll;
-  __shared__ f32x4_t red[kSkWaves][MT][64];
+    int64_t ldc, bool vec_store, int split, int dslabs, float* __restrict__ ws,
+    int* __restrict__ counters) {
+  constexpr int EPC = 16 / sizeof(TIn);  // elements per 16-byte half
+  constexpr int KD = 8 * EPC;            // k per double slab
+  constexpr int U = kSkU;
+  constexpr int NT = kSkNT;
+  __shared__ f32x4_t red[kSkWaves][MT][NT][64];
+  __shared__ int s_last;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int n0 = blockIdx.x * 16;
+  const int nb = blockIdx.x / split, sk = blockIdx.x % split;
+  const int n0 = nb * 16 * NT;
   const int r16 = lane & 15, g = lane >> 4;
+  const int kl = g * 2 * EPC;  // this lane's first k inside a double slab
   // Rows past N / M are clamped (loaded, never stored).
-  const TIn* wrow = W + static_cast<int64_t>(min(n0 + r16, N - 1)) * ldw + g * EPC;
+  const TIn* wrow[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) wrow[j] = W + static_cast<int64_t>(min(n0 + 16 * j + r16, N - 1)) * ldw;
   const TIn* arow[MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-    arow[mt] = A + static_cast<int64_t>(min(16 * mt + r16, M - 1)) * lda + g * EPC;
+  for (int mt = 0; mt < MT; ++mt) arow[mt] = A + static_cast<int64_t>(min(16 * mt + r16, M - 1)) * lda;
 
-  const int slabs = (K + KS - 1) / KS;
-  const int per = (slabs + kSkWaves - 1) / kSkWaves;
-  const int s0 = wave * per;
-  const int s1 = min(slabs, s0 + per);
+  const int per_blk = (dslabs + split - 1) / split;
+  const int d0 = sk * per_blk, d1 = min(dslabs, d0 + per_blk);
+  const int cnt = d1 > d0 ? d1 - d0 : 0;
+  const int per_w = (cnt + kSkWaves - 1) / kSkWaves;
+  const int w0 = d0 + wave * per_w, w1 = min(d1, w0 + per_w);
 
-  f32x4_t acc[MT];
+  f32x4_t acc[MT][NT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[mt][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int s = s0; s < s1; s += U) {
-    u32x4_t wf[U], af[U][MT];
+  for (int d = w0; d < w1; d += U) {
+    u32x4_t wf[U][NT][2], af[U][MT][2];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      // This lane's chunk starts at k = (s+u)*KS + g*EPC (the row pointers
-      // already hold g*EPC); chunks past K or past this wave's range load
-      // the row's first chunk and are zeroed.
-      const int k = (s + u) * KS + g * EPC;
-      const bool ok = (s + u < s1) && (k < K);
-      const int off = ok ? (s + u) * KS : -g * EPC;
-      wf[u] = *reinterpret_cast<const u32x4_t*>(wrow + off);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) af[u][mt] = *reinterpret_cast<const u32x4_t*>(arow[mt] + off);
-      if (!ok) {
-        wf[u] = u32x4_t{0u, 0u, 0u, 0u};
+      for (int h = 0; h < 2; ++h) {
+        // Halves past K or past this wave's range load the row's first
+        // chunk and are zeroed (K is a multiple of EPC).
+        const int k = (d + u) * KD + kl + h * EPC;
+        const bool ok = (d + u < w1) && (k < K);
+        const int off = ok ? k : 0;
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) af[u][mt] = u32x4_t{0u, 0u, 0u, 0u};
+        for (int j = 0; j < NT; ++j) wf[u][j][h] = *reinterpret_cast<const u32x4_t*>(wrow[j] + off);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) af[u][mt][h] = *reinterpret_cast<const u32x4_t*>(arow[mt] + off);
+        if (!ok) {
+#pragma unroll
+          for (int j = 0; j < NT; ++j) wf[u][j][h] = u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) af[u][mt][h] = u32x4_t{0u, 0u, 0u, 0u};
+        }
       }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) Mfma<TIn>::run(wf[u], af[u][mt], acc[mt]);
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int j = 0; j < NT; ++j) Mfma<TIn>::run(wf[u][j][h], af[u][mt][h], acc[mt][j]);
   }
 
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) red[wave][mt][lane] = acc[mt];
-  __syncthreads();
-  for (int mt = wave; mt < MT; mt += kSkWaves) {
-    f32x4_t t = red[0][mt][lane];
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int w = 1; w < kSkWaves; ++w) t += red[w][mt][lane];
-    const int m = 16 * mt + r16, n = n0 + 4 * g;
+    for (int j = 0; j < NT; ++j) red[wave][mt][j][lane] = acc[mt][j];
+  __syncthreads();
+
+  // One (m-tile, n-tile) pair per wave and pass: its sum over the waves.
+  constexpr int kPairs = MT * NT;
+  constexpr int kTile = kPairs * 64;  // f32x4 per block tile
+  f32x4_t sum[(kPairs + kSkWaves - 1) / kSkWaves];
+#pragma unroll
+  for (int q = 0; q < (kPairs + kSkWaves - 1) / kSkWaves; ++q) {
+    const int pr = wave + q * kSkWaves;
+    if (pr < kPairs) {
+      const int mt = pr / NT, j = pr % NT;
+      f32x4_t t = red[0][mt][j][lane];
+#pragma unroll
+      for (int w = 1; w < kSkWaves; ++w) t += red[w][mt][j][lane];
+      sum[q] = t;
+    }
+  }
+
+  if (split > 1) {
+    // Cross-block hand-off without cache-wide fences (an agent-scope fence
+    // writes back and invalidates this XCD's whole L2): partials are stored
+    // and loaded with agent-scope cache policy (sc1), which makes those
+    // accesses coherent across the XCDs' L2s, the same encoding the memory
+    // model uses for agent-scope atomic loads and stores.  The s_waitcnt
+    // before the barrier completes every thread's partial stores before
+    // thread 0 counts the block with a device atomic.
+    const __amdgpu_buffer_rsrc_t rws = __builtin_amdgcn_make_buffer_rsrc(
+        ws + static_cast<int64_t>(nb) * split * kTile * 4, 0, split * kTile * 16, 0x00020000);
+#pragma unroll
+    for (int q = 0; q < (kPairs + kSkWaves - 1) / kSkWaves; ++q) {
+      const int pr = wave + q * kSkWaves;
+      if (pr < kPairs)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, sum[q]), rws,
+                                               (sk * kTile + pr * 64 + lane) * 16, 0, kCpolSc1);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+      s_last = __hip_atomic_fetch_add(&counters[nb], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               split - 1;
+    __syncthreads();
+    if (!s_last) return;
+#pragma unroll
+    for (int q = 0; q < (kPairs + kSkWaves - 1) / kSkWaves; ++q) {
+      const int pr = wave + q * kSkWaves;
+      if (pr < kPairs) {
+        // All partials in flight at once, then summed in chunk order.
+        u32x4_t part[kSkMaxSplit];
+#pragma unroll
+        for (int c = 0; c < kSkMaxSplit; ++c)
+          if (c < split)
+            part[c] = __builtin_amdgcn_raw_buffer_load_b128(rws, (c * kTile + pr * 64 + lane) * 16, 0,
+                                                            kCpolSc1);
+        f32x4_t t = __builtin_bit_cast(f32x4_t, part[0]);
+#pragma unroll
+        for (int c = 1; c < kSkMaxSplit; ++c)
+          if (c < split) t += __builtin_bit_cast(f32x4_t, part[c]);
+        sum[q] = t;
+      }
+    }
+    if (threadIdx.x == 0)
+      __hip_atomic_store(&counters[nb], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+#pragma unroll
+  for (int q = 0; q < (kPairs + kSkWaves - 1) / kSkWaves; ++q) {
+    const int pr = wave + q * kSkWaves;
+    if (pr >= kPairs) continue;
+    const int mt = pr / NT, j = pr % NT;
+    const int m = 16 * mt + r16, n = n0 + 16 * j + 4 * g;
     float v[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      float x = t[r];
+      float x = sum[q][r];
       if (EPI != CGPT_EPI_NONE) x += n + r < N ? bias_value(bias, bias_bf16, n + r) : 0.f;
       if (EPI == CGPT_EPI_BIAS_GELU) x = gelu_tanh(x);
       v[r] = x;
@@ -119,36 +243,37 @@ __global__ __launch_bounds__(64 * kSkWaves) void gemm_skinny_kernel(
 }
 
 template <typename TIn, int EPI, typename TOut>
-static int launch_skinny_mt(const void* a, const void* w, const void* bias, bool bias_bf16, void* c,
-                            int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc,
-                            bool vec_store, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>((N + 15) / 16)), block(64 * kSkWaves);
+static int launch_skinny_mt(const SkinnyPlan& p, const void* a, const void* w, const void* bias,
+                            bool bias_bf16, void* c, int M, int N, int K, int64_t lda, int64_t ldw,
+                            int64_t ldc, bool vec_store, float* ws, int* counters, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(p.slices * p.split)), block(64 * kSkWaves);
   const TIn* A = static_cast<const TIn*>(a);
   const TIn* W = static_cast<const TIn*>(w);
   TOut* C = static_cast<TOut*>(c);
-  if (M <= 16)
+  if (p.mt == 1)
     hipLaunchKernelGGL((gemm_skinny_kernel<TIn, 1, EPI, TOut>), grid, block, 0, s, A, W, bias,
-                       bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store);
-  else if (M <= 32)
+                       bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store, p.split, p.dslabs, ws, counters);
+  else if (p.mt == 2)
     hipLaunchKernelGGL((gemm_skinny_kernel<TIn, 2, EPI, TOut>), grid, block, 0, s, A, W, bias,
-                       bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store);
+                       bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store, p.split, p.dslabs, ws, counters);
   else
     hipLaunchKernelGGL((gemm_skinny_kernel<TIn, 4, EPI, TOut>), grid, block, 0, s, A, W, bias,
-                       bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store);
+                       bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store, p.split, p.dslabs, ws, counters);
   return hip_status(hipGetLastError());
 }
 
 template <typename TIn, typename TOut>
-static int launch_skinny_epi(int epi, const void* a, const void* w, const void* bias, bool bias_bf16,
-                             void* c, int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc,
-                             bool vec_store, hipStream_t s) {
+static int launch_skinny_epi(const SkinnyPlan& p, int epi, const void* a, const void* w,
+                             const void* bias, bool bias_bf16, void* c, int M, int N, int K,
+                             int64_t lda, int64_t ldw, int64_t ldc, bool vec_store, float* ws,
+                             int* counters, hipStream_t s) {
   switch (epi) {
     case CGPT_EPI_NONE:
-      return launch_skinny_mt<TIn, CGPT_EPI_NONE, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, s);
+      return launch_skinny_mt<TIn, CGPT_EPI_NONE, TOut>(p, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s);
     case CGPT_EPI_BIAS:
-      return launch_skinny_mt<TIn, CGPT_EPI_BIAS, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, s);
+      return launch_skinny_mt<TIn, CGPT_EPI_BIAS, TOut>(p, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s);
     case CGPT_EPI_BIAS_GELU:
-      return launch_skinny_mt<TIn, CGPT_EPI_BIAS_GELU, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, s);
+      return launch_skinny_mt<TIn, CGPT_EPI_BIAS_GELU, TOut>(p, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s);
     default:
       return CGPT_EINVAL;
   }
@@ -156,15 +281,28 @@ static int launch_skinny_epi(int epi, const void* a, const void* w, const void* 
 
 int launch_gemm_skinny(bool bf16_in, int epilogue, const void* a, const void* w, const void* bias,
                        bool bias_bf16, void* c, bool out_bf16, int M, int N, int K, int64_t lda,
-                       int64_t ldw, int64_t ldc, hipStream_t s) {
+                       int64_t ldw, int64_t ldc, void* workspace, int64_t ws_bytes, int* counters,
+                       int64_t n_counters, hipStream_t s) {
   if (M > 64) return CGPT_ESHAPE;
+  SkinnyPlan p = skinny_plan(M, N, K, bf16_in ? 2 : 4, workspace != nullptr && counters != nullptr);
+  if (p.split > 1 && (p.ws_floats * 4 > ws_bytes || p.slices > n_counters ||
+                      (reinterpret_cast<uintptr_t>(workspace) & 15)))
+    return CGPT_EINVAL;
   const uintptr_t oa = out_bf16 ? 7 : 15;
   const bool vec_store = ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(c) & oa) == 0;
+  float* ws = static_cast<float*>(workspace);
   if (bf16_in)
-    return out_bf16 ? launch_skinny_epi<bf16_t, bf16_t>(epilogue, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, s)
-                    : launch_skinny_epi<bf16_t, float>(epilogue, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, s);
-  return out_bf16 ? launch_skinny_epi<float, bf16_t>(epilogue, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, s)
-                  : launch_skinny_epi<float, float>(epilogue, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, s);
+    return out_bf16 ? launch_skinny_epi<bf16_t, bf16_t>(p, epilogue, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s)
+                    : launch_skinny_epi<bf16_t, float>(p, epilogue, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s);
+  return out_bf16 ? launch_skinny_epi<float, bf16_t>(p, epilogue, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s)
+                  : launch_skinny_epi<float, float>(p, epilogue, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s);
+}
+
+int skinny_workspace(int M, int N, int K, bool bf16_in, int64_t* ws_bytes, int64_t* n_counters) {
+  const SkinnyPlan p = skinny_plan(M, N, K, bf16_in ? 2 : 4, true);
+  *ws_bytes = p.ws_floats * 4;
+  *n_counters = p.split > 1 ? p.slices : 0;
+  return CGPT_OK;
 }
 
 // ------------------------------------------------------- decode attention
@@ -208,8 +346,8 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(
   extern __shared__ float dsm[];
   float* qs = dsm;                     // hd
   float* sc = qs + hd;                 // Tmax scores, then probabilities
-  float* part = sc + Tmax;             // kDecThreads partial outputs
-  float* scr = part + kDecThreads;     // kDecWaves
+  float* part = sc + Tmax;             // kDecThreads * 8 partial outputs
+  float* scr = part + kDecThreads * 8; // kDecWaves
   const int tid = threadIdx.x;
   const int b = blockIdx.x / H, h = blockIdx.x % H;
   int pos = pos_base + (pos_dev != nullptr ? *pos_dev : 0);
@@ -253,17 +391,30 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(
   }
   sum = block_reduce<false>(sum, scr);  // its barriers also publish sc
 
-  // P V: thread (group gi, dim d) sums keys gi, gi + G, ...; P is rounded to
-  // the storage type before the product, as in the prefill kernel.
-  const int G = kDecThreads / hd, gi = tid / hd, d = tid % hd;
-  float acc = 0.f;
-  if (gi < G)
-    for (int j = gi; j < Tk; j += G) acc = fmaf(round_to<T>(sc[j]), Elem<T>::load(vcb + j * c_st + d), acc);
-  part[tid] = acc;
+  // P V: key group kg = tid / TPR handles keys kg, kg + KG, ...; its TPR
+  // threads each own EPV consecutive dims of the row (one 16-byte load per
+  // key).  P is rounded to the storage type before the product, as in the
+  // prefill kernel.  The KG group sums are then added through LDS.
+  const int tpr = hd / EPV;            // threads per value row
+  const int kgroups = kDecThreads / tpr;
+  const int kg = tid / tpr, c0 = (tid % tpr) * EPV;
+  float acc[EPV];
+#pragma unroll
+  for (int e = 0; e < EPV; ++e) acc[e] = 0.f;
+  for (int j = kg; j < Tk; j += kgroups) {
+    float vv[EPV];
+    load_vec(vcb + j * c_st + c0, vv);
+    const float p = round_to<T>(sc[j]);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) acc[e] = fmaf(p, vv[e], acc[e]);
+  }
+  // part holds kDecThreads * EPV floats: [group][dim]
+#pragma unroll
+  for (int e = 0; e < EPV; ++e) part[kg * hd + c0 + e] = acc[e];
   __syncthreads();
   if (tid < hd) {
     float t = 0.f;
-    for (int k = 0; k < G; ++k) t += part[k * hd + tid];
+    for (int k = 0; k < kgroups; ++k) t += part[k * hd + tid];
     Elem<T>::store(o + b * o_sb + h * o_sh + tid, t / sum);
   }
 }
@@ -354,13 +505,13 @@ extern "C" int cgpt_attention_decode(const void* q, const void* k_new, const voi
   if (dtype != CGPT_F32 && dtype != CGPT_BF16) return CGPT_EDTYPE;
   const int epv = dtype == CGPT_F32 ? 4 : 8;
   if (head_dim > kDecThreads || kDecThreads % head_dim != 0 || head_dim % epv != 0) return CGPT_ESHAPE;
-  if (t_max > 16384 || B * H > 0x7fffffff) return CGPT_ESHAPE;
+  if (t_max > 8192 || B * H > 0x7fffffff) return CGPT_ESHAPE;  // dynamic LDS <= 64 KiB
   // Cache rows are read as 16-byte vectors.
   if (c_st % epv != 0 || c_sh % epv != 0 || c_sb % epv != 0 || c_st < head_dim) return CGPT_EINVAL;
   if ((reinterpret_cast<uintptr_t>(k_cache) & 15) || (reinterpret_cast<uintptr_t>(v_cache) & 15))
     return CGPT_EINVAL;
   if (pos_dev == nullptr && (pos_base < 0 || pos_base >= t_max)) return CGPT_EINVAL;
-  const size_t smem = (static_cast<size_t>(head_dim) + t_max + kDecThreads + kDecWaves) * sizeof(float);
+  const size_t smem = (static_cast<size_t>(head_dim) + t_max + kDecThreads * 8 + kDecWaves) * sizeof(float);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const float sl2 = scale * 1.4426950408889634f;
   const int hh = static_cast<int>(H), hd = static_cast<int>(head_dim), tm = static_cast<int>(t_max);

@@ -800,10 +800,12 @@ static int launch_epi(int epi, int tile, const void* a, const void* w, const voi
 
 extern "C" int cgpt_gemm_num_tiles(void) { return cgpt::kNumBf16Tiles; }
 
-extern "C" int cgpt_gemm(const void* a, const void* w, const void* bias, void* c, int64_t M,
+namespace cgpt {
+// Argument checks shared by cgpt_gemm and cgpt_gemm_skinny: CGPT_OK when the
+// problem is well formed (M == 0 or N == 0 included: nothing to launch).
+static int validate_gemm(const void* a, const void* w, const void* bias, const void* c, int64_t M,
                          int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldc, int in_dtype,
-                         int bias_dtype, int out_dtype, int epilogue, int tile, void* stream) {
-  using namespace cgpt;
+                         int bias_dtype, int out_dtype, int epilogue) {
   if (M < 0 || N < 0 || K < 0) return CGPT_EINVAL;
   if (M == 0 || N == 0) return CGPT_OK;
   if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff) return CGPT_ESHAPE;
@@ -815,21 +817,59 @@ extern "C" int cgpt_gemm(const void* a, const void* w, const void* bias, void* c
   if (out_dtype != CGPT_F32 && out_dtype != CGPT_BF16) return CGPT_EDTYPE;
   if (epilogue != CGPT_EPI_NONE && bias_dtype != CGPT_F32 && bias_dtype != CGPT_BF16)
     return CGPT_EDTYPE;
-  const bool bf16 = in_dtype == CGPT_BF16;
-  const int64_t epc = bf16 ? 8 : 4;
+  const int64_t epc = in_dtype == CGPT_BF16 ? 8 : 4;
   if (K == 0 || K % epc != 0) return CGPT_ESHAPE;
   if (lda < K || ldw < K || ldc < N) return CGPT_EINVAL;
   if (lda % epc != 0 || ldw % epc != 0) return CGPT_EINVAL;
   if ((reinterpret_cast<uintptr_t>(a) & 15) || (reinterpret_cast<uintptr_t>(w) & 15))
     return CGPT_EINVAL;
   if (epilogue != CGPT_EPI_NONE && (reinterpret_cast<uintptr_t>(bias) & 15)) return CGPT_EINVAL;
+  return CGPT_OK;
+}
+}  // namespace cgpt
+
+extern "C" int cgpt_gemm_skinny_workspace(int64_t M, int64_t N, int64_t K, int in_dtype,
+                                          int64_t* workspace_bytes, int64_t* n_counters) {
+  using namespace cgpt;
+  if (!workspace_bytes || !n_counters || M <= 0 || M > 64 || N <= 0 || K <= 0) return CGPT_EINVAL;
+  if (N > 0x7fffffff || K > 0x7fffffff) return CGPT_ESHAPE;
+  if (in_dtype != CGPT_F32 && in_dtype != CGPT_BF16) return CGPT_EDTYPE;
+  return skinny_workspace(static_cast<int>(M), static_cast<int>(N), static_cast<int>(K),
+                          in_dtype == CGPT_BF16, workspace_bytes, n_counters);
+}
+
+extern "C" int cgpt_gemm_skinny(const void* a, const void* w, const void* bias, void* c, int64_t M,
+                                int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldc,
+                                int in_dtype, int bias_dtype, int out_dtype, int epilogue,
+                                void* workspace, int64_t workspace_bytes, int* counters,
+                                int64_t n_counters, void* stream) {
+  using namespace cgpt;
+  const int st = validate_gemm(a, w, bias, c, M, N, K, lda, ldw, ldc, in_dtype, bias_dtype,
+                               out_dtype, epilogue);
+  if (st != CGPT_OK || M == 0 || N == 0) return st;
+  if (M > 64) return CGPT_ESHAPE;
+  return launch_gemm_skinny(in_dtype == CGPT_BF16, epilogue, a, w, bias, bias_dtype == CGPT_BF16,
+                            c, out_dtype == CGPT_BF16, static_cast<int>(M), static_cast<int>(N),
+                            static_cast<int>(K), lda, ldw, ldc, workspace, workspace_bytes, counters,
+                            n_counters, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int cgpt_gemm(const void* a, const void* w, const void* bias, void* c, int64_t M,
+                         int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldc, int in_dtype,
+                         int bias_dtype, int out_dtype, int epilogue, int tile, void* stream) {
+  using namespace cgpt;
+  const int st = validate_gemm(a, w, bias, c, M, N, K, lda, ldw, ldc, in_dtype, bias_dtype,
+                               out_dtype, epilogue);
+  if (st != CGPT_OK || M == 0 || N == 0) return st;
+  const bool bf16 = in_dtype == CGPT_BF16;
   const int nt = bf16 ? kNumBf16Tiles : kNumF32Tiles;
   if (tile == CGPT_TILE_AUTO && M <= 64) tile = CGPT_TILE_SKINNY;
   if (tile == CGPT_TILE_SKINNY) {
     if (M > 64) return CGPT_ESHAPE;
     return launch_gemm_skinny(bf16, epilogue, a, w, bias, bias_dtype == CGPT_BF16, c,
                               out_dtype == CGPT_BF16, static_cast<int>(M), static_cast<int>(N),
-                              static_cast<int>(K), lda, ldw, ldc, static_cast<hipStream_t>(stream));
+                              static_cast<int>(K), lda, ldw, ldc, nullptr, 0, nullptr, 0,
+                              static_cast<hipStream_t>(stream));
   }
   if (tile == CGPT_TILE_AUTO)
     tile = auto_tile(bf16, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K));

@@ -6,12 +6,16 @@
 
 namespace cgpt {
 
-// Skinny GEMM (M <= 64): C[M,N] = epilogue(A W^T + bias), one 16-column slice of
-// C per block, K split across the block's waves and reduced through LDS.
-// Arguments as cgpt_gemm's, already validated (K % (16 / element size) == 0,
-// 16-byte aligned A and W rows).
+// Skinny GEMM (M <= 64): C[M,N] = epilogue(A W^T + bias).  64-column slices of
+// C, K split across the block's waves and (when workspace and counters are
+// given) across blocks.  Arguments as cgpt_gemm's, already validated
+// (K % (16 / element size) == 0, 16-byte aligned A and W rows).
 int launch_gemm_skinny(bool bf16_in, int epilogue, const void* a, const void* w, const void* bias,
                        bool bias_bf16, void* c, bool out_bf16, int M, int N, int K, int64_t lda,
-                       int64_t ldw, int64_t ldc, hipStream_t s);
+                       int64_t ldw, int64_t ldc, void* workspace, int64_t ws_bytes, int* counters,
+                       int64_t n_counters, hipStream_t s);
+
+// Workspace bytes and counters the split-K skinny GEMM uses for (M, N, K).
+int skinny_workspace(int M, int N, int K, bool bf16_in, int64_t* ws_bytes, int64_t* n_counters);
 
 }  // namespace cgpt

@@ -27,12 +27,21 @@ __device__ __forceinline__ void store4(bf16_t* p, const float* v) {
   *reinterpret_cast<u32x2_t*>(p) = u;
 }
 
-__device__ __forceinline__ void load4_param(const void* p, bool bf16, int64_t col, float* v) {
-  if (bf16) load4(static_cast<const bf16_t*>(p) + col, v);
-  else load4(static_cast<const float*>(p) + col, v);
+// gamma / beta: 16 raw bytes from the chunk's first element through a buffer
+// resource (fp32: 4 values; bf16: the first 8 bytes), decoded by the uniform
+// type flag after the load, so no branch separates a load from its use.
+__device__ __forceinline__ void decode_param(u32x4_t r, bool bf16, float* v) {
+  if (bf16) {
+    v[0] = __uint_as_float(r[0] << 16);
+    v[1] = __uint_as_float(r[0] & 0xffff0000u);
+    v[2] = __uint_as_float(r[1] << 16);
+    v[3] = __uint_as_float(r[1] & 0xffff0000u);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = __uint_as_float(r[j]);
+  }
 }
 
-// MAXCH = upper bound on 256-column chunks per row (cols <= 256 * MAXCH).
 template <typename TX, typename TD, typename TY, int MAXCH>
 __global__ __launch_bounds__(kLnThreads) void add_layernorm_kernel(
     const TX* __restrict__ x, const TD* __restrict__ delta, TX* x_out,
@@ -42,54 +51,70 @@ __global__ __launch_bounds__(kLnThreads) void add_layernorm_kernel(
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kLnRowsPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int64_t base = row * cols;
-  const int nch = (cols + 255) / 256;
+  const int pshift = param_bf16 ? 1 : 2;
+  const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(gamma), 0, cols << pshift, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(beta), 0, cols << pshift, 0x00020000);
 
-  float v[MAXCH][4];
+  // Every load of the row is issued before any is used, with no branch around
+  // it: columns past the row load column 0 and are masked, so the wave's
+  // loads (x, delta, gamma, beta) are in flight together — one memory round
+  // trip, which is what short batches (decode steps) are bound by.
+  // Without delta the x row is loaded a second time in its place (same bytes,
+  // discarded by a select), so the loads stay unconditional.
+  const bool has_delta = delta != nullptr;
+  const TD* dsrc = has_delta ? delta : reinterpret_cast<const TD*>(x);
+  const int64_t dbase = has_delta ? base : 0;
+  float v[MAXCH][4], dv[MAXCH][4], gm[MAXCH][4], bt[MAXCH][4];
+  u32x4_t graw[MAXCH], braw[MAXCH];
   float sum = 0.f;
 #pragma unroll
   for (int c = 0; c < MAXCH; ++c) {
     const int col = (c * 64 + lane) * 4;
-    if (c < nch && col < cols) {
-      load4(x + base + col, v[c]);
-      if (delta != nullptr) {
-        float d[4];
-        load4(delta + base + col, d);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[c][j] += d[j];
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) sum += v[c][j];
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[c][j] = 0.f;
-    }
+    const int cc = col < cols ? col : 0;
+    load4(x + base + cc, v[c]);
+    load4(dsrc + dbase + (has_delta ? cc : 0), dv[c]);
+    graw[c] = __builtin_amdgcn_raw_buffer_load_b128(rg, cc << pshift, 0, 0);
+    braw[c] = __builtin_amdgcn_raw_buffer_load_b128(rb, cc << pshift, 0, 0);
   }
-  const float inv_n = 1.0f / static_cast<float>(cols);
-  const float mean = wave_sum(sum) * inv_n;
+#pragma unroll
+  for (int c = 0; c < MAXCH; ++c) {
+    const bool ok = (c * 64 + lane) * 4 < cols;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float t = v[c][j] + (has_delta ? dv[c][j] : 0.f);
+      v[c][j] = ok ? t : 0.f;
+      sum += v[c][j];
+    }
+    decode_param(graw[c], param_bf16, gm[c]);
+    decode_param(braw[c], param_bf16, bt[c]);
+  }
+  // Correctly rounded divisions (not a multiply by 1/cols, which the compiler
+  // may fuse into x - mean): a constant row then gives mean == x exactly and
+  // y == beta.
+  const float n_f = static_cast<float>(cols);
+  const float mean = wave_sum(sum) / n_f;
   float sq = 0.f;
 #pragma unroll
   for (int c = 0; c < MAXCH; ++c) {
-    const int col = (c * 64 + lane) * 4;
-    if (c < nch && col < cols) {
+    const bool ok = (c * 64 + lane) * 4 < cols;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float t = v[c][j] - mean;
-        sq += t * t;
-      }
+    for (int j = 0; j < 4; ++j) {
+      const float t = v[c][j] - mean;
+      sq += ok ? t * t : 0.f;
     }
   }
-  const float var = wave_sum(sq) * inv_n;
+  const float var = wave_sum(sq) / n_f;
   const float rstd = 1.0f / sqrtf(var + eps);
 #pragma unroll
   for (int c = 0; c < MAXCH; ++c) {
     const int col = (c * 64 + lane) * 4;
-    if (c < nch && col < cols) {
+    if (col < cols) {
       if (x_out != nullptr) store4(x_out + base + col, v[c]);
-      float g[4], b[4], o[4];
-      load4_param(gamma, param_bf16, col, g);
-      load4_param(beta, param_bf16, col, b);
+      float o[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) o[j] = (v[c][j] - mean) * rstd * g[j] + b[j];
+      for (int j = 0; j < 4; ++j) o[j] = (v[c][j] - mean) * rstd * gm[c][j] + bt[c][j];
       store4(y + base + col, o);
     }
   }

@@ -22,6 +22,7 @@ dtype, t_max = prompt length + new tokens (<= block_size).
 
 from __future__ import annotations
 
+import ctypes
 import math
 from typing import Optional
 
@@ -74,6 +75,18 @@ class DecodeSession:
         self.logits = torch.empty((B, V), dtype=model.logits_dtype, device=dev)
         self.err = torch.zeros(1, dtype=torch.int32, device=dev)
         self.graph: Optional[torch.cuda.CUDAGraph] = None
+        # One split-K workspace + counter array serves every step GEMM (they
+        # run one after another on one stream and leave the counters zero).
+        lib = _lib.load()
+        ws_max, cnt_max = 0, 0
+        for n, k in ((3 * D, D), (D, D), (4 * D, D), (D, 4 * D), (V, D)):
+            wb, nc = ctypes.c_int64(), ctypes.c_int64()
+            _lib.check(lib.cgpt_gemm_skinny_workspace(B, n, k, _DT[act], ctypes.byref(wb),
+                                                      ctypes.byref(nc)), "skinny workspace")
+            ws_max, cnt_max = max(ws_max, wb.value), max(cnt_max, nc.value)
+        self.ws = torch.empty(max(ws_max // 4, 4), dtype=torch.float32, device=dev)
+        self.ws_bytes = self.ws.numel() * 4
+        self.counters = torch.zeros(max(cnt_max, 1), dtype=torch.int32, device=dev)
 
     # ----------------------------------------------------------------- prefill
 
@@ -104,16 +117,19 @@ class DecodeSession:
         B, D, H, V, hd = self.B, cfg.n_embd, cfg.n_head, cfg.vocab_size, self.hd
         ac = _DT[m.dtype]
         f32 = _lib.CGPT_F32
-        skinny = _lib.TILE_SKINNY
         s = torch.cuda.current_stream(m.device).cuda_stream
         px, ph, pq, pa, pd, pf = (t.data_ptr() for t in (self.x, self.h, self.qkv, self.att,
                                                          self.delta, self.f))
         pstep = self.step.data_ptr()
         esz = self.qkv.element_size()
 
+        pws, pcnt, nws, ncnt = (self.ws.data_ptr(), self.counters.data_ptr(), self.ws_bytes,
+                                self.counters.numel())
+
         def gemm(a_ptr, w, b, c_ptr, n, k, epi, out_code):
-            chk(lib.cgpt_gemm(a_ptr, w.data_ptr(), None if b is None else b.data_ptr(), c_ptr,
-                              B, n, k, k, w.stride(0), n, ac, ac, out_code, epi, skinny, s), "gemm")
+            chk(lib.cgpt_gemm_skinny(a_ptr, w.data_ptr(), None if b is None else b.data_ptr(),
+                                     c_ptr, B, n, k, k, w.stride(0), n, ac, ac, out_code, epi,
+                                     pws, nws, pcnt, ncnt, s), "gemm_skinny")
 
         def add_ln(delta_ptr, wk):
             chk(lib.cgpt_add_layernorm(px, delta_ptr, px if delta_ptr else None,

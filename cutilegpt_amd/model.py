@@ -41,7 +41,7 @@ class CutileGPT:
 
     def __init__(self, config: GPTConfig, dtype: torch.dtype = torch.float32,
                  device: str = "cuda", seed: Optional[int] = None,
-                 logits_dtype: torch.dtype = torch.float32):
+                 logits_dtype: torch.dtype = torch.float32, init_weights: bool = True):
         if dtype not in _DT:
             raise ValueError(f"dtype must be float32 or bfloat16, got {dtype}")
         if config.n_embd % config.n_head:
@@ -52,7 +52,8 @@ class CutileGPT:
         self.logits_dtype = logits_dtype
         self.weights: Dict[str, torch.Tensor] = {}
         self._err = None
-        self._init_weights(seed)
+        if init_weights:
+            self._init_weights(seed)
 
     # ------------------------------------------------------------------ weights
 

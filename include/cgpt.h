@@ -100,6 +100,29 @@ int cgpt_gemm(const void* a, const void* w, const void* bias, void* c,
 int cgpt_gemm_num_tiles(void);
 
 /*
+ * The skinny GEMM (M <= 64, e.g. one decode step's rows) with its K range also
+ * split across blocks.  Same arguments and checks as cgpt_gemm, plus a caller
+ * workspace (16-byte aligned, >= the bytes cgpt_gemm_skinny_workspace reports)
+ * and n_counters ints that must be zero before the first call; every call
+ * leaves them zero again, so they can be reused (and captured in a graph)
+ * without clearing.  Partials are combined in a fixed order: results are
+ * deterministic and identical to the tile = CGPT_TILE_SKINNY path's up to
+ * summation order.  Calls sharing a workspace must not run concurrently.
+ * workspace = NULL runs the unsplit kernel.  Replaces cutile_linear /
+ * cutile_linear_bias at decode shapes (cutile_gpt/kernels/linear.py:112-222,
+ * called per token by generate, cutile_gpt/models/gpt.py:185-229).
+ */
+int cgpt_gemm_skinny(const void* a, const void* w, const void* bias, void* c,
+                     int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldc,
+                     int in_dtype, int bias_dtype, int out_dtype, int epilogue,
+                     void* workspace, int64_t workspace_bytes, int* counters,
+                     int64_t n_counters, void* stream);
+
+/* Workspace bytes and counters cgpt_gemm_skinny needs for (M, N, K, in_dtype). */
+int cgpt_gemm_skinny_workspace(int64_t M, int64_t N, int64_t K, int in_dtype,
+                               int64_t* workspace_bytes, int64_t* n_counters);
+
+/*
  * Causal (or full) softmax attention, O = softmax(Q K^T * scale + mask) V,
  * for B batches x H heads; Q has Tq rows, K/V have Tk rows (Tk >= Tq); query i
  * sits at absolute position Tk - Tq + i and, when `causal`, sees keys j <= that
@@ -157,7 +180,7 @@ int cgpt_embedding_at(const int64_t* idx, const void* wte, const void* wpe, void
  * pos, then o = softmax(q K[0..pos]^T * scale) V[0..pos] — the causal row of
  * position pos.  P is rounded to `dtype` before the P*V product, as in
  * cgpt_attention_fwd.  head_dim divides 256 and is a multiple of 8 (bf16) / 4
- * (fp32); t_max <= 16384.  A device pos outside [0, t_max) is clamped and sets
+ * (fp32); t_max <= 8192.  A device pos outside [0, t_max) is clamped and sets
  * *err_flag.  Replaces the per-token full recompute of cutile_causal_attention
  * inside generate (cutile_gpt/models/gpt.py:185-229, attention.py:119-175).
  */

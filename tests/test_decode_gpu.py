@@ -7,6 +7,7 @@ level checks use tighter ones where noted); bf16 outputs within 3e-2 or a few
 bf16 ulps of the exact (fp64) result.
 """
 
+import ctypes
 import math
 
 import pytest
@@ -76,6 +77,64 @@ def test_skinny_auto_tile_and_limits(gpu):
                                  _lib.EPI_NONE, tile, stream(gpu)), "gemm")
     torch.cuda.synchronize()
     assert torch.equal(c1, c2)
+
+
+def skinny_ws(lib, M, N, K, dtype, gpu):
+    wb, nc = ctypes.c_int64(), ctypes.c_int64()
+    _lib.check(lib.cgpt_gemm_skinny_workspace(M, N, K, DT[dtype], ctypes.byref(wb),
+                                              ctypes.byref(nc)), "ws")
+    ws = torch.empty(max(wb.value // 4, 4), dtype=torch.float32, device=gpu)
+    cnt = torch.zeros(max(nc.value, 1), dtype=torch.int32, device=gpu)
+    return ws, cnt, nc.value
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("M,N,K", [(32, 1600, 1600), (32, 1600, 6400), (32, 4800, 1600),
+                                   (7, 6400, 1600), (64, 130, 4096), (1, 50, 520)])
+def test_skinny_split_k_matches_unsplit(gpu, dtype, M, N, K):
+    """Split-K with the last-block fix-up: same result as fp64 within the
+    unsplit tolerance, identical across repeated calls (the counters reset
+    themselves), and within summation-order noise of the unsplit kernel."""
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(N + K + M)
+    a = torch.randn(M, K, generator=g).to(dtype)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(dtype)
+    b = torch.randn(N, generator=g).to(dtype)
+    ref = R.gelu_tanh(a.double() @ w.double().t() + b.double())
+    ws, cnt, ncnt = skinny_ws(lib, M, N, K, dtype, gpu)
+    ad, wd, bd = a.to(gpu), w.to(gpu), b.to(gpu)
+    outs = []
+    for _ in range(3):
+        c = torch.full((M, N), float("nan"), device=gpu)
+        _lib.check(lib.cgpt_gemm_skinny(ad.data_ptr(), wd.data_ptr(), bd.data_ptr(), c.data_ptr(),
+                                        M, N, K, K, K, N, DT[dtype], DT[dtype], _lib.CGPT_F32,
+                                        _lib.EPI_BIAS_GELU, ws.data_ptr(), ws.numel() * 4,
+                                        cnt.data_ptr(), cnt.numel(), stream(gpu)), "skinny split")
+        outs.append(c)
+    c1 = torch.empty((M, N), device=gpu)
+    _lib.check(lib.cgpt_gemm(ad.data_ptr(), wd.data_ptr(), bd.data_ptr(), c1.data_ptr(), M, N, K, K,
+                             K, N, DT[dtype], DT[dtype], _lib.CGPT_F32, _lib.EPI_BIAS_GELU,
+                             _lib.TILE_SKINNY, stream(gpu)), "skinny")
+    torch.cuda.synchronize()
+    assert (cnt == 0).all()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    scale = ref.abs().max().item() + 1.0
+    assert (outs[0].double().cpu() - ref).abs().max().item() <= 1e-4 * scale
+    assert (outs[0] - c1).abs().max().item() <= 1e-4 * scale
+
+
+def test_skinny_split_k_rejects_small_workspace(gpu):
+    lib = _lib.load()
+    M, N, K = 32, 1600, 6400
+    ws, cnt, ncnt = skinny_ws(lib, M, N, K, torch.bfloat16, gpu)
+    assert ncnt > 0
+    a = torch.zeros(M, K, device=gpu, dtype=torch.bfloat16)
+    w = torch.zeros(N, K, device=gpu, dtype=torch.bfloat16)
+    c = torch.empty(M, N, device=gpu)
+    st = lib.cgpt_gemm_skinny(a.data_ptr(), w.data_ptr(), None, c.data_ptr(), M, N, K, K, K, N,
+                              _lib.CGPT_BF16, _lib.CGPT_BF16, _lib.CGPT_F32, _lib.EPI_NONE,
+                              ws.data_ptr(), 16, cnt.data_ptr(), cnt.numel(), stream(gpu))
+    assert st == -1
 
 
 # ------------------------------------------------------------- decode attention
