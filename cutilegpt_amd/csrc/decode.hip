@@ -444,21 +444,34 @@ __global__ __launch_bounds__(256) void kv_store_kernel(
 
 // ------------------------------------------------------------------- argmax
 
+constexpr int kAmThreads = 1024;
+constexpr int kAmUnroll = 8;
+
 template <typename T>
-__global__ __launch_bounds__(256) void argmax_kernel(const T* __restrict__ x, int64_t ld, int cols,
-                                                     int64_t* __restrict__ ids, int64_t* __restrict__ hist,
-                                                     int64_t hist_ld, const int* __restrict__ step_dev) {
-  __shared__ float sv[4];
-  __shared__ int si[4];
+__global__ __launch_bounds__(kAmThreads) void argmax_kernel(const T* __restrict__ x, int64_t ld, int cols,
+                                                            int64_t* __restrict__ ids, int64_t* __restrict__ hist,
+                                                            int64_t hist_ld, const int* __restrict__ step_dev) {
+  constexpr int NW = kAmThreads / 64;
+  __shared__ float sv[NW];
+  __shared__ int si[NW];
   const T* row = x + static_cast<int64_t>(blockIdx.x) * ld;
   float best = -INFINITY;
   int bi = INT_MAX;
-  for (int c = threadIdx.x; c < cols; c += 256) {
-    const float v = Elem<T>::load(row + c);
-    if (v > best) {  // ascending scan: the first maximum wins
-      best = v;
-      bi = c;
+  // kAmUnroll independent loads per thread in flight; each thread scans its
+  // columns in ascending order, so the first maximum wins within a thread.
+  for (int c0 = threadIdx.x; c0 < cols; c0 += kAmThreads * kAmUnroll) {
+    float v[kAmUnroll];
+#pragma unroll
+    for (int u = 0; u < kAmUnroll; ++u) {
+      const int c = c0 + u * kAmThreads;
+      v[u] = c < cols ? Elem<T>::load(row + c) : -INFINITY;
     }
+#pragma unroll
+    for (int u = 0; u < kAmUnroll; ++u)
+      if (v[u] > best) {
+        best = v[u];
+        bi = c0 + u * kAmThreads;
+      }
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
@@ -476,7 +489,7 @@ __global__ __launch_bounds__(256) void argmax_kernel(const T* __restrict__ x, in
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < 4; ++w)
+    for (int w = 1; w < NW; ++w)
       if (sv[w] > best || (sv[w] == best && si[w] < bi)) {
         best = sv[w];
         bi = si[w];
@@ -576,10 +589,10 @@ extern "C" int cgpt_argmax(const void* x, int64_t rows, int64_t cols, int64_t ld
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int c = static_cast<int>(cols);
   if (dtype == CGPT_F32)
-    hipLaunchKernelGGL(argmax_kernel<float>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s,
+    hipLaunchKernelGGL(argmax_kernel<float>, dim3(static_cast<unsigned>(rows)), dim3(kAmThreads), 0, s,
                        static_cast<const float*>(x), ld, c, ids, hist, hist_ld, step_dev);
   else if (dtype == CGPT_BF16)
-    hipLaunchKernelGGL(argmax_kernel<bf16_t>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s,
+    hipLaunchKernelGGL(argmax_kernel<bf16_t>, dim3(static_cast<unsigned>(rows)), dim3(kAmThreads), 0, s,
                        static_cast<const bf16_t*>(x), ld, c, ids, hist, hist_ld, step_dev);
   else
     return CGPT_EDTYPE;
