@@ -30,7 +30,10 @@
 
 namespace cgpt {
 
-constexpr int kGroupM = 8;
+#ifndef CGPT_GROUP_M
+#define CGPT_GROUP_M 8
+#endif
+constexpr int kGroupM = CGPT_GROUP_M;
 constexpr int kNumXcd = 8;
 
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -307,17 +310,19 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 // Wait until the stage that has `later` stages of LPS loads each issued after
 // it, plus (when `stores`) ST stores, has landed: vmcnt retires loads and
-// stores in issue order.
+// stores in issue order.  Counts past the 6-bit counter's range wait for 63
+// (a stronger condition).
+constexpr int vm_cap(int n) { return n < 63 ? n : 63; }
 template <int LPS, int MAXLATER, int ST>
 __device__ __forceinline__ void wait_stages(int later, bool stores) {
   static_assert(MAXLATER <= 4, "up to 6 stages");
-  static_assert(MAXLATER * LPS + ST < 64, "vmcnt range");
+  static_assert(MAXLATER * LPS < 64, "vmcnt range");
   if (stores) {
-    if constexpr (MAXLATER >= 4) if (later >= 4) { wait_vmcnt<4 * LPS + ST>(); return; }
-    if constexpr (MAXLATER >= 3) if (later >= 3) { wait_vmcnt<3 * LPS + ST>(); return; }
-    if constexpr (MAXLATER >= 2) if (later >= 2) { wait_vmcnt<2 * LPS + ST>(); return; }
-    if constexpr (MAXLATER >= 1) if (later >= 1) { wait_vmcnt<1 * LPS + ST>(); return; }
-    wait_vmcnt<ST>();
+    if constexpr (MAXLATER >= 4) if (later >= 4) { wait_vmcnt<vm_cap(4 * LPS + ST)>(); return; }
+    if constexpr (MAXLATER >= 3) if (later >= 3) { wait_vmcnt<vm_cap(3 * LPS + ST)>(); return; }
+    if constexpr (MAXLATER >= 2) if (later >= 2) { wait_vmcnt<vm_cap(2 * LPS + ST)>(); return; }
+    if constexpr (MAXLATER >= 1) if (later >= 1) { wait_vmcnt<vm_cap(1 * LPS + ST)>(); return; }
+    wait_vmcnt<vm_cap(ST)>();
     return;
   }
   if constexpr (MAXLATER >= 4) if (later >= 4) { wait_vmcnt<4 * LPS>(); return; }
@@ -354,7 +359,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
   static_assert(STAGES >= 2 && STAGES <= 6, "2..6 stages");
   static_assert(SPS == 2 || STAGES % 2 == 0, "single-slab stages alternate fragment sets");
   static_assert(BM % (RPI * NW) == 0 && BN % (RPI * NW) == 0, "tile/wave mismatch");
-  static_assert((STAGES - 2) * LPS + TM * TN < 64, "vmcnt range");
+  static_assert((STAGES - 2) * LPS < 64, "vmcnt range");
   __shared__ __attribute__((aligned(1024))) uint8_t st0[STAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t st1[STAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t st2[STAGES > 2 ? STAGE : 16];
@@ -443,27 +448,25 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
       for (int j = 0; j < TN; ++j) Mfma<bf16_t>::run(f.w[j], f.a[i], acc[i][j]);
   };
 
-  // Bias of the tile being computed, reloaded at every step (before the
-  // step's DMA, so the loads are older than everything a wait counts) and
-  // used by the epilogue at the tile's last step.  With buffer stores N % 4 ==
-  // 0, so each 4-column group is one aligned vector load with no branch on the
-  // bias type (groups past N read the last group); otherwise each element's
-  // dword is loaded, clamped into [0, N): byte (n+r)*4 (fp32) or
-  // ((n+r)*2) & ~3 (bf16, half by parity).
+  // Bias of a tile, loaded once per tile: tile 0's before the prologue, tile
+  // i+1's right after tile i's epilogue stores (clamped to the last tile, so
+  // the loads are unconditional).  The registers stay live until the next
+  // epilogue, so the compiler never waits on them except before that first
+  // use.  With buffer stores N % 4 == 0, so each 4-column group is one
+  // aligned vector load with no branch on the bias type (groups past N read
+  // the last group); otherwise each element's dword is loaded, clamped into
+  // [0, N): byte (n+r)*4 (fp32) or ((n+r)*2) & ~3 (bf16, half by parity).
   uint32_t braw[TN][4];
-  int cmp_n0;
-  {
-    int tm, tn;
-    tile_coords(static_cast<int>(blockIdx.x), tiles_m, tiles_n, tm, tn);
-    cmp_n0 = tn * BN;
-  }
   const int bshift = bias_bf16 ? 1 : 2;
   const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<void*>(bias), 0, EPI != CGPT_EPI_NONE ? N << bshift : 0, kBufferRsrcWord3);
-  auto load_bias = [&]() {
+  auto load_bias = [&](int i) {
+    int tm, tn;
+    tile_coords(static_cast<int>(blockIdx.x) + min(i, n_mine - 1) * static_cast<int>(gridDim.x),
+                tiles_m, tiles_n, tm, tn);
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const int n = cmp_n0 + wn0 + j * 16 + 4 * fgrp;
+      const int n = tn * BN + wn0 + j * 16 + 4 * fgrp;
       if constexpr (BUFST) {
         // 16 bytes from the group's first element whatever the type (bf16
         // uses the first 8); bytes past the bias read as zero.
@@ -563,14 +566,16 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
 
   Frag fr;
   int cmp_i = 0, cmp_kt = 0;
+  // Memory operations a buffer-store epilogue issues: its stores and the next
+  // tile's bias loads.
+  constexpr int EPI_OPS = TM * TN + (EPI != CGPT_EPI_NONE ? TN : 0);
   // Wait until stage `h` has landed: `later` stages issued after it may stay
-  // in flight, and so may the exact TM * TN buffer stores of an epilogue
-  // issued after them.
-  auto wait_for = [&](int h, bool stores) {
+  // in flight, and so may the exact EPI_OPS operations of a buffer-store
+  // epilogue issued after them.
+  auto wait_for = [&](int h, bool epi) {
     int later = total - 1 - h;
     later = later < STAGES - 2 ? later : STAGES - 2;
-    // Younger than stage h: `later` stages, and possibly an epilogue's stores.
-    wait_stages<LPS, STAGES - 2, TM * TN>(later, stores);
+    wait_stages<LPS, STAGES - 2, EPI_OPS>(later, epi);
   };
   // One flattened step g on stage buffer `cur`; `dst` receives stage
   // g + STAGES - 1.  Every wave enters having waited for stage g itself; the
@@ -580,7 +585,6 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
   auto step = [&](const uint8_t* cur, uint8_t* dst, int g) {
     raw_barrier();
     const bool last = cmp_kt == KT - 1;
-    if (EPI != CGPT_EPI_NONE) load_bias();
     if (g + STAGES - 1 < total) issue(dst);
 #pragma unroll
     for (int s = 0; s < SPS; ++s) {
@@ -588,27 +592,24 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
       mma_slab(fr);
     }
     if (last) {
-      if (epilogue(cmp_i)) {
-        zero_acc();
+      const bool buf = epilogue(cmp_i);
+      if (EPI != CGPT_EPI_NONE) load_bias(cmp_i + 1);
+      zero_acc();
+      if (buf)
         wait_for(g + 1, true);
-      } else {
-        zero_acc();
+      else
         wait_vmcnt<0>();
-      }
     } else {
       wait_for(g + 1, false);
     }
     if (++cmp_kt == KT) {
       cmp_kt = 0;
       ++cmp_i;
-      int tm, tn;
-      tile_coords(static_cast<int>(blockIdx.x) + cmp_i * static_cast<int>(gridDim.x), tiles_m, tiles_n,
-                  tm, tn);
-      cmp_n0 = tn * BN;
     }
   };
 
   zero_acc();
+  if (EPI != CGPT_EPI_NONE) load_bias(0);
   set_offsets(0);
   auto bufp = [&](int b) -> uint8_t* {
     return b == 0 ? st0 : b == 1 ? st1 : b == 2 ? st2 : b == 3 ? st3 : b == 4 ? st4 : st5;
@@ -621,6 +622,230 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
 #pragma unroll
     for (int j = 0; j < STAGES; ++j)
       if (g0 + j < total) step(bufp(j), bufp((j + STAGES - 1) % STAGES), g0 + j);
+  }
+#endif  // __HIP_DEVICE_COMPILE__
+}
+
+// The same persistent pipeline with the A (activation) operand fetched one
+// step further ahead than W: A rotates through 3 LDS buffers, W through 2, and
+// each step issues W(g+1) then A(g+2), so the A rows — most of an XCD's L2
+// misses, since each A block is shared by 4 CUs of a round and each W block
+// by 8 — get two steps to arrive.  k = 64 per stage (SPS 2).
+template <int BM, int BN, int WGM, int WGN, int EPI, typename TOut>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_a3_kernel(
+    const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, const void* __restrict__ bias,
+    bool bias_bf16, TOut* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldw,
+    int64_t ldc, int tiles_m, int tiles_n, bool vec_store) {
+  // The body uses AMDGPU-only types (buffer resources); the host pass only
+  // needs the kernel's signature for its launch stub.
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int NT = 64 * WGM * WGN, NW = NT / 64;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int TM = WM / 16, TN = WN / 16;
+  constexpr int SPS = 2;
+  constexpr int ROWB = 64 * SPS;           // bytes of K per LDS row per stage
+  constexpr int CPR = ROWB / 16;           // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;            // rows filled by one wave DMA instruction
+  constexpr int ABUF = BM * ROWB, WBUF = BN * ROWB;
+  constexpr int A_INS = BM / (RPI * NW);
+  constexpr int W_INS = BN / (RPI * NW);
+  static_assert(BM % (RPI * NW) == 0 && BN % (RPI * NW) == 0, "tile/wave mismatch");
+  static_assert(A_INS < 64, "vmcnt range");
+  // A buffers 0..2, then W buffers 0..1 (the DMA writes them through M0, so
+  // one array with computed offsets is all the compiler needs to see).
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[3 * ABUF + 2 * WBUF];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
+  const int frow = lane & 15, fgrp = lane >> 4;
+  const int lrow = lane / CPR, pchunk = lane % CPR;
+  auto swz = [](int row) { return ROWB == 128 ? (row & 7) : ((row >> 1) & 3); };
+
+  const u32x4_t ra = buffer_desc(A, static_cast<uint32_t>(static_cast<int64_t>(M) * lda * 2));
+  const u32x4_t rw = buffer_desc(W, static_cast<uint32_t>(static_cast<int64_t>(N) * ldw * 2));
+
+  const int n_tiles = tiles_m * tiles_n;
+  const int KT = K / (32 * SPS);
+  const int n_mine = (n_tiles - 1 - static_cast<int>(blockIdx.x)) / static_cast<int>(gridDim.x) + 1;
+  const int total = n_mine * KT;
+
+  // ---- issue side: one cursor per operand (A runs a stage ahead of W)
+  int ia_i = 0, ia_kt = 0, iw_i = 0, iw_kt = 0;
+  uint32_t aoff[A_INS], woff[W_INS];
+  auto tile_of = [&](int i, int& tm, int& tn) {
+    tile_coords(static_cast<int>(blockIdx.x) + i * static_cast<int>(gridDim.x), tiles_m, tiles_n,
+                tm, tn);
+  };
+  auto set_a = [&](int i) {
+    int tm, tn;
+    tile_of(i, tm, tn);
+#pragma unroll
+    for (int ii = 0; ii < A_INS; ++ii) {
+      const int row = (ii * NW + wave) * RPI + lrow;
+      const int64_t g = min(tm * BM + row, M - 1);
+      aoff[ii] = static_cast<uint32_t>(g * lda * 2 + ((pchunk ^ swz(row)) << 4));
+    }
+  };
+  auto set_w = [&](int i) {
+    int tm, tn;
+    tile_of(i, tm, tn);
+#pragma unroll
+    for (int ii = 0; ii < W_INS; ++ii) {
+      const int row = (ii * NW + wave) * RPI + lrow;
+      const int64_t g = min(tn * BN + row, N - 1);
+      woff[ii] = static_cast<uint32_t>(g * ldw * 2 + ((pchunk ^ swz(row)) << 4));
+    }
+  };
+  auto issue_a = [&](int b) {
+    uint8_t* buf = smem + b * ABUF;
+#pragma unroll
+    for (int ii = 0; ii < A_INS; ++ii)
+      dma_lds16(ra, lds_addr(buf + (ii * NW + wave) * 1024), aoff[ii], ia_kt * ROWB);
+    if (++ia_kt == KT) {
+      ia_kt = 0;
+      if (++ia_i < n_mine) set_a(ia_i);
+    }
+  };
+  auto issue_w = [&](int b) {
+    uint8_t* buf = smem + 3 * ABUF + b * WBUF;
+#pragma unroll
+    for (int ii = 0; ii < W_INS; ++ii)
+      dma_lds16(rw, lds_addr(buf + (ii * NW + wave) * 1024), woff[ii], iw_kt * ROWB);
+    if (++iw_kt == KT) {
+      iw_kt = 0;
+      if (++iw_i < n_mine) set_w(iw_i);
+    }
+  };
+
+  // ---- compute side
+  f32x4_t acc[TM][TN];
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  };
+  // Byte offset of this lane's fragment row inside a stage, per slab.
+  int xo[SPS];
+#pragma unroll
+  for (int s = 0; s < SPS; ++s) xo[s] = ((4 * s + fgrp) ^ swz(frow)) << 4;
+  const int a_base = (wm0 + frow) * ROWB, w_base = (wn0 + frow) * ROWB;
+  struct Frag {
+    u32x4_t a[TM], w[TN];
+  };
+  auto read_slab = [&](const uint8_t* abuf, const uint8_t* wbuf, int s, Frag& f) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      f.a[i] = *reinterpret_cast<const u32x4_t*>(abuf + a_base + i * 16 * ROWB + xo[s]);
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      f.w[j] = *reinterpret_cast<const u32x4_t*>(wbuf + w_base + j * 16 * ROWB + xo[s]);
+  };
+  auto mma_slab = [&](const Frag& f) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) Mfma<bf16_t>::run(f.w[j], f.a[i], acc[i][j]);
+  };
+
+  // Bias of a tile, loaded once per tile as in gemm_pipe_kernel (N % 4 == 0:
+  // one 16-byte load per 4-column group, groups past N read the last group).
+  uint32_t braw[TN][4];
+  const int bshift = bias_bf16 ? 1 : 2;
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(bias), 0, EPI != CGPT_EPI_NONE ? N << bshift : 0, kBufferRsrcWord3);
+  auto load_bias = [&](int i) {
+    int tm, tn;
+    tile_of(min(i, n_mine - 1), tm, tn);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = tn * BN + wn0 + j * 16 + 4 * fgrp;
+      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rb, min(n, N - 4) << bshift, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) braw[j][r] = v[r];
+    }
+  };
+  auto bias_at = [&](int j, int r) -> float {
+    if (!bias_bf16) return __uint_as_float(braw[j][r]);
+    const uint32_t w = braw[j][r >> 1];
+    return __uint_as_float((r & 1) ? (w & 0xffff0000u) : (w << 16));
+  };
+  // Exactly TM * TN buffer stores per wave: rows past M lie past the
+  // resource's size and columns past N get an offset past it, so both are
+  // dropped, and the next wait can leave the stores in flight.
+  auto epilogue = [&](int i) {
+    int tm, tn;
+    tile_of(i, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int rows = min(BM, M - m0);
+    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+        C + static_cast<int64_t>(m0) * ldc, 0,
+        static_cast<int>(static_cast<int64_t>(rows) * ldc * static_cast<int64_t>(sizeof(TOut))),
+        kBufferRsrcWord3);
+#pragma unroll
+    for (int ii = 0; ii < TM; ++ii) {
+      const uint32_t roff = static_cast<uint32_t>((wm0 + ii * 16 + frow) * ldc);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = n0 + wn0 + j * 16 + 4 * fgrp;
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float t = acc[ii][j][r];
+          if (EPI != CGPT_EPI_NONE) t += bias_at(j, r);
+          if (EPI == CGPT_EPI_BIAS_GELU) t = gelu_tanh(t);
+          v[r] = t;
+        }
+        const uint32_t off =
+            n < N ? (roff + static_cast<uint32_t>(n)) * static_cast<uint32_t>(sizeof(TOut)) : 0x80000000u;
+        buffer_store4(rc, off, v, static_cast<TOut*>(nullptr));
+      }
+    }
+  };
+
+  Frag fr;
+  int cmp_i = 0, cmp_kt = 0;
+  // After step g: A(g+1) and W(g+1) must have landed; only A(g+2) (issued
+  // last in step g) and the epilogue's stores and bias loads may stay in
+  // flight.
+  constexpr int EPI_OPS = TM * TN + (EPI != CGPT_EPI_NONE ? TN : 0);
+  auto wait_next = [&](int g, bool epi) {
+    wait_stages<A_INS, 1, EPI_OPS>(g + 2 < total ? 1 : 0, epi);
+  };
+  int ab = 0, wb = 0;  // buffers of stage g: A g % 3, W g % 2
+  zero_acc();
+  if (EPI != CGPT_EPI_NONE) load_bias(0);
+  set_a(0);
+  set_w(0);
+  // Prologue: W(0), A(0), A(1); wait for W(0), A(0).
+  if (total > 0) issue_w(0);
+  if (total > 0) issue_a(0);
+  if (total > 1) issue_a(1);
+  wait_stages<A_INS, 1, EPI_OPS>(total > 1 ? 1 : 0, false);
+  for (int g = 0; g < total; ++g) {
+    raw_barrier();
+    const bool last = cmp_kt == KT - 1;
+    if (g + 1 < total) issue_w(wb ^ 1);
+    if (g + 2 < total) issue_a(ab == 0 ? 2 : ab - 1);
+    const uint8_t* abuf = smem + ab * ABUF;
+    const uint8_t* wbuf = smem + 3 * ABUF + wb * WBUF;
+#pragma unroll
+    for (int s = 0; s < SPS; ++s) {
+      read_slab(abuf, wbuf, s, fr);
+      mma_slab(fr);
+    }
+    if (last) {
+      epilogue(cmp_i);
+      if (EPI != CGPT_EPI_NONE) load_bias(cmp_i + 1);
+      zero_acc();
+    }
+    wait_next(g, last);
+    if (++cmp_kt == KT) {
+      cmp_kt = 0;
+      ++cmp_i;
+    }
+    ab = ab == 2 ? 0 : ab + 1;
+    wb ^= 1;
   }
 #endif  // __HIP_DEVICE_COMPILE__
 }
@@ -649,9 +874,11 @@ static const TileCfg kBf16Tiles[] = {
     {256, 128, 4, 2},  // 9: 8 waves (64x64),  SPS 2, 3 stages, 144 KiB
     {128, 256, 2, 4},  // 10: 8 waves (64x64), SPS 2, 3 stages, 144 KiB
     {256, 128, 4, 2},  // 11: 8 waves (64x64), SPS 1, 6 stages, 144 KiB
+    {256, 256, 2, 4},  // 12: 8 waves (128x64), A 3 buffers / W 2, 160 KiB
+    {256, 192, 2, 4},  // 13: 8 waves (128x48), A 3 buffers / W 2, 144 KiB
 };
 constexpr int kFirstPipeTile = 5;
-static const int kPipeSps[] = {2, 1, 2, 2, 2, 2, 1};
+static const int kPipeSps[] = {2, 1, 2, 2, 2, 2, 1, 2, 2};
 // fp32 configurations (index = tile id for CGPT_F32).
 static const TileCfg kF32Tiles[] = {
     {128, 128, 2, 2},  // 0
@@ -718,8 +945,33 @@ static int launch_pipe(const void* a, const void* w, const void* bias, bool bias
   return hip_status(hipGetLastError());
 }
 
-// The pipelined kernel addresses A and W through 32-bit buffer offsets and
-// consumes K in whole stages.
+// A fetched two steps ahead (3 A buffers, 2 W buffers, k = 64 per stage).  It
+// only has the buffer-store epilogue; other output layouts take the two-stage
+// kernel of the same tile.
+template <int BM, int BN, int WGM, int WGN, int EPI, typename TOut>
+static int launch_pipe_a3(const void* a, const void* w, const void* bias, bool bias_bf16, void* c,
+                          int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc,
+                          bool vec_store, hipStream_t s) {
+  static_assert((3 * BM + 2 * BN) * 128 <= 160 * 1024, "LDS budget of one CU");
+  const bool buf_store = vec_store && N % 4 == 0 &&
+                         static_cast<int64_t>(BM) * ldc * static_cast<int64_t>(sizeof(TOut)) < 0x7fffffff;
+  if (!buf_store)
+    return launch_pipe<BM, BN, WGM, WGN, 2, 2, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda,
+                                                          ldw, ldc, vec_store, s);
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = (N + BN - 1) / BN;
+  const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
+  if (tiles > 0x7fffffff) return CGPT_ESHAPE;
+  const int grid = static_cast<int>(tiles < num_cus() ? tiles : num_cus());
+  hipLaunchKernelGGL((gemm_pipe_a3_kernel<BM, BN, WGM, WGN, EPI, TOut>), dim3(grid),
+                     dim3(64 * WGM * WGN), 0, s, static_cast<const bf16_t*>(a),
+                     static_cast<const bf16_t*>(w), bias, bias_bf16, static_cast<TOut*>(c), M, N,
+                     K, lda, ldw, ldc, tiles_m, tiles_n, vec_store);
+  return hip_status(hipGetLastError());
+}
+
+// The pipelined kernels address A and W through 32-bit buffer offsets and
+// consume K in whole stages.
 static bool pipe_ok(int tile, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) {
   const int sps = kPipeSps[tile - kFirstPipeTile];
   return K % (32 * sps) == 0 && M * lda * 2 < 0x7fffffff && N * ldw * 2 < 0x7fffffff;
@@ -751,6 +1003,13 @@ static int launch_tile(int tile, const void* a, const void* w, const void* bias,
       CGPT_PIPE_CASE(9, 256, 128, 4, 2, 2, 3)
       CGPT_PIPE_CASE(10, 128, 256, 2, 4, 2, 3)
       CGPT_PIPE_CASE(11, 256, 128, 4, 2, 1, 6)
+      case 12:
+        return launch_pipe_a3<256, 256, 2, 4, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda,
+                                                         ldw, ldc, vec_store, s);
+      case 13:
+        return launch_pipe_a3<256, 192, 2, 4, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda,
+                                                         ldw, ldc, vec_store, s);
+
       default: return CGPT_EINVAL;
     }
   } else {

@@ -112,6 +112,25 @@ class CutileGPT:
         for k, shp in expect.items():
             if tuple(out[k].shape) != shp:
                 raise ValueError(f"{k} has shape {tuple(out[k].shape)}, expected {shp}")
+        # The LM head's B operand padded with zero rows to a multiple of 64
+        # (50257 -> 50304): the head GEMM then has N % 64 == 0, every output
+        # row is 16-byte aligned (vector and buffer-resource stores) and the
+        # 256x192 tiles cover it exactly.  wte (and a tied lm_head) are views
+        # of the first vocab_size rows, so nothing is duplicated.
+        V, D = cfg.vocab_size, cfg.n_embd
+        vp = (V + 63) // 64 * 64
+        tied = out["lm_head.weight"] is out["wte"]
+        if vp == V:
+            self._head_pad = out["lm_head.weight"]
+        else:
+            pad = torch.zeros((vp, D), dtype=self.dtype, device=self.device)
+            pad[:V].copy_(out["lm_head.weight"])
+            self._head_pad = pad
+            if tied:
+                out["wte"] = pad[:V]
+                out["lm_head.weight"] = out["wte"]
+            else:
+                out["lm_head.weight"] = pad[:V]
         self.weights = out
 
     @property
@@ -177,7 +196,8 @@ class CutileGPT:
         att = torch.empty((M, D), dtype=act, device=dev)
         delta = torch.empty((M, D), dtype=act, device=dev)
         f = torch.empty((M, 4 * D), dtype=act, device=dev)
-        logits = (torch.empty((M, V), dtype=self.logits_dtype, device=dev)
+        Vp = self._head_pad.shape[0]
+        logits = (torch.empty((M, Vp), dtype=self.logits_dtype, device=dev)
                   if logits_out is None else None)
         px, ph, pq, pa, pd, pf = (t.data_ptr() for t in (x, h, qkv, att, delta, f))
 
@@ -238,9 +258,15 @@ class CutileGPT:
                               _lib.EPI_NONE, _lib.TILE_AUTO, s), "lm_head")
             mark("lm_head", False)
             return logits_out
-        gemm("lm_head", ph, W["lm_head.weight"], None, logits.data_ptr(), V, D, _lib.EPI_NONE,
-             _DT[self.logits_dtype])
-        return logits.view(B, T, V)
+        # Padded head: logits rows have stride Vp; the returned (B, T, V) tensor
+        # is a view of the first V columns.
+        mark("lm_head", True)
+        head = self._head_pad
+        chk(lib.cgpt_gemm(ph, head.data_ptr(), None, logits.data_ptr(), M, Vp, D, D, head.stride(0),
+                          Vp, ac, ac, _DT[self.logits_dtype], _lib.EPI_NONE,
+                          gemm_tile(ac, M, Vp, D), s), "lm_head")
+        mark("lm_head", False)
+        return logits[:, :V].view(B, T, V)
 
     def input_errors(self) -> bool:
         """True if any forward so far saw a token id outside the vocabulary

@@ -15,6 +15,9 @@ Tile ids index the configuration table compiled into libcgpt.so
           7 = 256x192, 2 stages of 2 (128x48/wave) 8 = 256x192 (64x96/wave), 2 of 2
           9 = 256x128, 3 stages of 2               10 = 128x256, 3 stages of 2
           11 = 256x128, 6 stages of 1
+    bf16, the same pipeline with A fetched two steps ahead (3 A buffers,
+    2 W buffers, 2 k32 slabs per stage; buffer-store outputs only):
+          12 = 256x256                             13 = 256x192
     fp32: 0 = 128x128, 1 = 64x64
 
 ``TABLE`` maps exact (dtype, M, N, K) problems measured on MI355X to the tile
@@ -33,16 +36,16 @@ from . import _lib
 _B = _lib.CGPT_BF16
 TABLE: Dict[Tuple[int, int, int, int], int] = {
     # GPT-2 124M prefill, M = 16 x 1024
-    (_B, 16384, 2304, 768): 7,    # c_attn       758
-    (_B, 16384, 768, 768): 7,     # attn c_proj  713
-    (_B, 16384, 3072, 768): 7,    # c_fc         814
-    (_B, 16384, 768, 3072): 7,    # mlp c_proj  1073
-    (_B, 16384, 50257, 768): 5,   # lm head      650 (bf16 out)
+    (_B, 16384, 2304, 768): 7,    # c_attn       797
+    (_B, 16384, 768, 768): 7,     # attn c_proj  741
+    (_B, 16384, 3072, 768): 12,   # c_fc         901
+    (_B, 16384, 768, 3072): 7,    # mlp c_proj  1147
+    (_B, 16384, 50304, 768): 12,  # lm head (vocab padded), fp32 out 809
     # 'medium' (8L, d 512) prefill, M = 16 x 256
-    (_B, 4096, 1536, 512): 10,    # 397
-    (_B, 4096, 2048, 512): 10,    # 515
+    (_B, 4096, 1536, 512): 10,    # 420
+    (_B, 4096, 2048, 512): 10,    # 532
     (_B, 4096, 512, 2048): 3,     # 271
-    (_B, 4096, 50257, 512): 5,    # 516
+    (_B, 4096, 50304, 512): 5,    # lm head (vocab padded), fp32 out 666
 }
 
 

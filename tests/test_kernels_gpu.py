@@ -131,7 +131,7 @@ def test_gemm_every_bf16_tile(gpu, tile, m, n, k):
     close(out, gemm_ref(a, w, b, _lib.EPI_BIAS), 1e-3, 2 ** -8, f"tile {tile}")
 
 
-DMA_TILES = [5, 6, 7, 8, 9, 10, 11]
+DMA_TILES = [5, 6, 7, 8, 9, 10, 11, 12, 13]
 
 
 @pytest.mark.parametrize("tile", DMA_TILES)
@@ -148,12 +148,13 @@ def test_gemm_dma_tiles(gpu, tile, m, n, k, epi):
     close(out, ref, 1e-4 * math.sqrt(k / 64), 1e-5, f"dma tile {tile} {m}x{n}x{k}")
 
 
-PERSIST_TILES = [5, 7, 9, 10, 11]
+PERSIST_TILES = [5, 7, 9, 10, 11, 12, 13]
 
 
 @pytest.mark.parametrize("tile", PERSIST_TILES)
 @pytest.mark.parametrize("m,n,k", [(300, 520, 128), (4096, 4096, 256), (257, 50257, 192),
-                                   (16384, 768, 3072), (1, 3, 128)])
+                                   (16384, 768, 3072), (1, 3, 128), (1000, 1000, 64),
+                                   (2000, 50304, 64)])
 @pytest.mark.parametrize("epi", [_lib.EPI_BIAS, _lib.EPI_BIAS_GELU])
 def test_gemm_persistent_tiles(gpu, tile, m, n, k, epi):
     """Persistent kernel: several tiles per block (tile boundaries inside the
