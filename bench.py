@@ -45,7 +45,7 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # Bytes beyond L2 per LM-head launch (2.0 x FETCH_SIZE + 1.0 x WRITE_SIZE, factors from
 # a 1 GiB copy), measured with rocprofv3 --pmc on the GPT-2 workload; see
 # profiles/lm_head_gemm_gpt2_traffic_pmc.md.  Only valid for the gpt2 workload.
-LM_HEAD_TRAFFIC_BYTES = 5.28e9
+LM_HEAD_TRAFFIC_BYTES = 5.17e9
 
 WORKLOADS = {
     "gpt2": dict(n_layer=12, n_head=12, n_embd=768, batch=16, seq=1024,
