@@ -231,22 +231,30 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
       // or the end of the sequence.
       constexpr float kLazyLog2 = 8.0f;
       const bool need_mask = (causal && kv0 + BKV - 1 > wave_q0 + off) || (kv0 + BKV > Tk);
+      // Masking is a separate pass over the scores, taken by one wave-uniform
+      // branch, so blocks off the diagonal run straight-line code with no
+      // per-element key arithmetic.  Key kv0 + 4g + 16kt + r survives iff
+      // 16kt + r <= lim, lim being the row's last visible key relative to
+      // kv0 + 4g.
+      if (need_mask) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          const int qpos = wave_q0 + qt * 16 + frow + off;
+          const int lim = (causal ? min(qpos, Tk - 1) : Tk - 1) - kv0 - 4 * g;
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              s[qt][kt][r] = (kt * 16 + r > lim) ? -INFINITY : s[qt][kt][r];
+        }
+      }
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) {
-        const int qpos = wave_q0 + qt * 16 + frow + off;
         float mloc = -INFINITY;
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float x = s[qt][kt][r];
-            if (need_mask) {
-              const int key = kv0 + kt * 16 + 4 * g + r;
-              x = (key >= Tk || (causal && key > qpos)) ? -INFINITY : x;
-              s[qt][kt][r] = x;
-            }
-            mloc = fmaxf(mloc, x);
-          }
+          for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, s[qt][kt][r]);
         mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
         const float mblk = mloc * scale_log2;  // scale > 0: max commutes

@@ -357,15 +357,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
   constexpr int LPS = A_INS + W_INS;       // DMA instructions per wave per stage
   static_assert(SPS == 1 || SPS == 2, "one or two k32 slabs per stage");
   static_assert(STAGES >= 2 && STAGES <= 6, "2..6 stages");
-  static_assert(SPS == 2 || STAGES % 2 == 0, "single-slab stages alternate fragment sets");
   static_assert(BM % (RPI * NW) == 0 && BN % (RPI * NW) == 0, "tile/wave mismatch");
   static_assert((STAGES - 2) * LPS < 64, "vmcnt range");
-  __shared__ __attribute__((aligned(1024))) uint8_t st0[STAGE];
-  __shared__ __attribute__((aligned(1024))) uint8_t st1[STAGE];
-  __shared__ __attribute__((aligned(1024))) uint8_t st2[STAGES > 2 ? STAGE : 16];
-  __shared__ __attribute__((aligned(1024))) uint8_t st3[STAGES > 3 ? STAGE : 16];
-  __shared__ __attribute__((aligned(1024))) uint8_t st4[STAGES > 4 ? STAGE : 16];
-  __shared__ __attribute__((aligned(1024))) uint8_t st5[STAGES > 5 ? STAGE : 16];
+  // Stage buffers at computed offsets in one array (the DMA writes them
+  // through M0, so the compiler sees only the fragment reads).
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE];
   __shared__ float escr[NW][kScrFloats];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -565,7 +561,6 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
   };
 
   Frag fr;
-  int cmp_i = 0, cmp_kt = 0;
   // Memory operations a buffer-store epilogue issues: its stores and the next
   // tile's bias loads.
   constexpr int EPI_OPS = TM * TN + (EPI != CGPT_EPI_NONE ? TN : 0);
@@ -577,51 +572,50 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
     later = later < STAGES - 2 ? later : STAGES - 2;
     wait_stages<LPS, STAGES - 2, EPI_OPS>(later, epi);
   };
-  // One flattened step g on stage buffer `cur`; `dst` receives stage
-  // g + STAGES - 1.  Every wave enters having waited for stage g itself; the
-  // barrier makes all waves' parts of it visible.  The step ends with the
-  // tile's epilogue when it is the tile's last, then waits for stage g + 1 in
-  // the same straight-line code as the stores, so the wait can count them.
-  auto step = [&](const uint8_t* cur, uint8_t* dst, int g) {
-    raw_barrier();
-    const bool last = cmp_kt == KT - 1;
-    if (g + STAGES - 1 < total) issue(dst);
-#pragma unroll
-    for (int s = 0; s < SPS; ++s) {
-      read_slab(cur, s, fr);
-      mma_slab(fr);
-    }
-    if (last) {
-      const bool buf = epilogue(cmp_i);
-      if (EPI != CGPT_EPI_NONE) load_bias(cmp_i + 1);
-      zero_acc();
-      if (buf)
-        wait_for(g + 1, true);
-      else
-        wait_vmcnt<0>();
-    } else {
-      wait_for(g + 1, false);
-    }
-    if (++cmp_kt == KT) {
-      cmp_kt = 0;
-      ++cmp_i;
-    }
-  };
-
-  zero_acc();
-  if (EPI != CGPT_EPI_NONE) load_bias(0);
+  // Tile loop around a K-step loop, so the accumulators are zeroed at the top
+  // of a tile and carried in place through its steps (no select between the
+  // running sums and zero inside the step loop).  The DMA stream is flat:
+  // step g (global over this block's tiles) reads stage buffer g % STAGES
+  // and issues stage g + STAGES - 1, which may belong to the next tile.  Every
+  // wave enters a step having waited for its own part of stage g; the
+  // barrier makes all waves' parts visible.  After a tile's epilogue the wait
+  // for the next stage runs in the same straight-line code as the stores, so
+  // it can leave them in flight.
   set_offsets(0);
-  auto bufp = [&](int b) -> uint8_t* {
-    return b == 0 ? st0 : b == 1 ? st1 : b == 2 ? st2 : b == 3 ? st3 : b == 4 ? st4 : st5;
-  };
+  if (EPI != CGPT_EPI_NONE) load_bias(0);
+  int ib = 0;  // stage buffer the next issue fills
+  auto next_buf = [](int b) { return b + 1 == STAGES ? 0 : b + 1; };
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
-    if (s < total) issue(bufp(s));
+    if (s < total) {
+      issue(smem + ib * STAGE);
+      ib = next_buf(ib);
+    }
   wait_for(0, false);
-  for (int g0 = 0; g0 < total; g0 += STAGES) {
+  int cb = 0, g = 0;  // stage buffer being read, flattened step
+  for (int t = 0; t < n_mine; ++t) {
+    zero_acc();
+    for (int kt = 0; kt < KT; ++kt, ++g) {
+      raw_barrier();
+      if (g + STAGES - 1 < total) {
+        issue(smem + ib * STAGE);
+        ib = next_buf(ib);
+      }
+      const uint8_t* cur = smem + cb * STAGE;
 #pragma unroll
-    for (int j = 0; j < STAGES; ++j)
-      if (g0 + j < total) step(bufp(j), bufp((j + STAGES - 1) % STAGES), g0 + j);
+      for (int s = 0; s < SPS; ++s) {
+        read_slab(cur, s, fr);
+        mma_slab(fr);
+      }
+      cb = next_buf(cb);
+      if (kt + 1 < KT) wait_for(g + 1, false);
+    }
+    const bool buf = epilogue(t);
+    if (EPI != CGPT_EPI_NONE) load_bias(t + 1);
+    if (buf)
+      wait_for(g, true);
+    else
+      wait_vmcnt<0>();
   }
 #endif  // __HIP_DEVICE_COMPILE__
 }
@@ -804,7 +798,6 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_a3_kernel(
   };
 
   Frag fr;
-  int cmp_i = 0, cmp_kt = 0;
   // After step g: A(g+1) and W(g+1) must have landed; only A(g+2) (issued
   // last in step g) and the epilogue's stores and bias loads may stay in
   // flight.
@@ -813,7 +806,6 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_a3_kernel(
     wait_stages<A_INS, 1, EPI_OPS>(g + 2 < total ? 1 : 0, epi);
   };
   int ab = 0, wb = 0;  // buffers of stage g: A g % 3, W g % 2
-  zero_acc();
   if (EPI != CGPT_EPI_NONE) load_bias(0);
   set_a(0);
   set_w(0);
@@ -822,30 +814,224 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_a3_kernel(
   if (total > 0) issue_a(0);
   if (total > 1) issue_a(1);
   wait_stages<A_INS, 1, EPI_OPS>(total > 1 ? 1 : 0, false);
-  for (int g = 0; g < total; ++g) {
-    raw_barrier();
-    const bool last = cmp_kt == KT - 1;
-    if (g + 1 < total) issue_w(wb ^ 1);
-    if (g + 2 < total) issue_a(ab == 0 ? 2 : ab - 1);
-    const uint8_t* abuf = smem + ab * ABUF;
-    const uint8_t* wbuf = smem + 3 * ABUF + wb * WBUF;
+  // Tile loop around the K-step loop (accumulators zeroed per tile, carried
+  // in place), flat DMA stream as in gemm_pipe_kernel.
+  int g = 0;
+  for (int t = 0; t < n_mine; ++t) {
+    zero_acc();
+    for (int kt = 0; kt < KT; ++kt, ++g) {
+      raw_barrier();
+      if (g + 1 < total) issue_w(wb ^ 1);
+      if (g + 2 < total) issue_a(ab == 0 ? 2 : ab - 1);
+      const uint8_t* abuf = smem + ab * ABUF;
+      const uint8_t* wbuf = smem + 3 * ABUF + wb * WBUF;
 #pragma unroll
-    for (int s = 0; s < SPS; ++s) {
-      read_slab(abuf, wbuf, s, fr);
-      mma_slab(fr);
+      for (int s = 0; s < SPS; ++s) {
+        read_slab(abuf, wbuf, s, fr);
+        mma_slab(fr);
+      }
+      ab = ab == 2 ? 0 : ab + 1;
+      wb ^= 1;
+      if (kt + 1 < KT) wait_next(g, false);
     }
-    if (last) {
-      epilogue(cmp_i);
-      if (EPI != CGPT_EPI_NONE) load_bias(cmp_i + 1);
-      zero_acc();
+    epilogue(t);
+    if (EPI != CGPT_EPI_NONE) load_bias(t + 1);
+    wait_next(g - 1, true);
+  }
+#endif  // __HIP_DEVICE_COMPILE__
+}
+
+// Two stages of k = 64 (2 k32 slabs each) with the LDS fragment reads
+// software-pipelined one slab ahead of the MFMAs, so no MFMA waits for an LDS
+// read it has just issued:
+//   step g:  read slab 1 of stage g      | MFMAs of slab 0 of stage g
+//            wait (own DMA of stage g+1, own reads of stage g), barrier,
+//            DMA stage g+2 into stage g's buffer,
+//            read slab 0 of stage g+1    | MFMAs of slab 1 of stage g
+//            [last step of a tile: epilogue, next tile's bias]
+// The barrier sits between the two slabs: once every wave has read all of
+// stage g its buffer can be refilled.  Buffer-resource stores only.
+template <int BM, int BN, int WGM, int WGN, int EPI, typename TOut>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_slab_kernel(
+    const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, const void* __restrict__ bias,
+    bool bias_bf16, TOut* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldw,
+    int64_t ldc, int tiles_m, int tiles_n, bool vec_store) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int NT = 64 * WGM * WGN, NW = NT / 64;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int TM = WM / 16, TN = WN / 16;
+  constexpr int ROWB = 128, CPR = 8, RPI = 8;  // k = 64 per LDS row
+  constexpr int STAGE = (BM + BN) * ROWB;
+  constexpr int A_INS = BM / (RPI * NW), W_INS = BN / (RPI * NW);
+  static_assert(BM % (RPI * NW) == 0 && BN % (RPI * NW) == 0, "tile/wave mismatch");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
+  const int frow = lane & 15, fgrp = lane >> 4;
+  const int lrow = lane / CPR, pchunk = lane % CPR;
+
+  const u32x4_t ra = buffer_desc(A, static_cast<uint32_t>(static_cast<int64_t>(M) * lda * 2));
+  const u32x4_t rw = buffer_desc(W, static_cast<uint32_t>(static_cast<int64_t>(N) * ldw * 2));
+
+  const int n_tiles = tiles_m * tiles_n;
+  const int KT = K / 64;
+  const int n_mine = (n_tiles - 1 - static_cast<int>(blockIdx.x)) / static_cast<int>(gridDim.x) + 1;
+  const int total = n_mine * KT;
+  auto tile_of = [&](int i, int& tm, int& tn) {
+    tile_coords(static_cast<int>(blockIdx.x) + i * static_cast<int>(gridDim.x), tiles_m, tiles_n,
+                tm, tn);
+  };
+
+  // ---- issue side (flat stage stream over this block's tiles)
+  int iss_i = 0, iss_kt = 0;
+  uint32_t aoff[A_INS], woff[W_INS];
+  auto set_offsets = [&](int i) {
+    int tm, tn;
+    tile_of(i, tm, tn);
+#pragma unroll
+    for (int ii = 0; ii < A_INS; ++ii) {
+      const int row = (ii * NW + wave) * RPI + lrow;
+      const int64_t g = min(tm * BM + row, M - 1);
+      aoff[ii] = static_cast<uint32_t>(g * lda * 2 + ((pchunk ^ (row & 7)) << 4));
     }
-    wait_next(g, last);
-    if (++cmp_kt == KT) {
-      cmp_kt = 0;
-      ++cmp_i;
+#pragma unroll
+    for (int ii = 0; ii < W_INS; ++ii) {
+      const int row = (ii * NW + wave) * RPI + lrow;
+      const int64_t g = min(tn * BN + row, N - 1);
+      woff[ii] = static_cast<uint32_t>(g * ldw * 2 + ((pchunk ^ (row & 7)) << 4));
     }
-    ab = ab == 2 ? 0 : ab + 1;
-    wb ^= 1;
+  };
+  auto issue = [&](uint8_t* buf) {
+    const int soff = iss_kt * ROWB;
+#pragma unroll
+    for (int ii = 0; ii < A_INS; ++ii)
+      dma_lds16(ra, lds_addr(buf + (ii * NW + wave) * 1024), aoff[ii], soff);
+#pragma unroll
+    for (int ii = 0; ii < W_INS; ++ii)
+      dma_lds16(rw, lds_addr(buf + BM * ROWB + (ii * NW + wave) * 1024), woff[ii], soff);
+    if (++iss_kt == KT) {
+      iss_kt = 0;
+      if (++iss_i < n_mine) set_offsets(iss_i);
+    }
+  };
+
+  // ---- compute side
+  f32x4_t acc[TM][TN];
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  };
+  const int xo0 = (fgrp ^ (frow & 7)) << 4, xo1 = ((4 + fgrp) ^ (frow & 7)) << 4;
+  const int a_base = (wm0 + frow) * ROWB, w_base = BM * ROWB + (wn0 + frow) * ROWB;
+  struct Frag {
+    u32x4_t a[TM], w[TN];
+  };
+  auto read_slab = [&](const uint8_t* buf, int xo, Frag& f) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      f.a[i] = *reinterpret_cast<const u32x4_t*>(buf + a_base + i * 16 * ROWB + xo);
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      f.w[j] = *reinterpret_cast<const u32x4_t*>(buf + w_base + j * 16 * ROWB + xo);
+  };
+  auto mma_slab = [&](const Frag& f) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) Mfma<bf16_t>::run(f.w[j], f.a[i], acc[i][j]);
+  };
+
+  uint32_t braw[TN][4];
+  const int bshift = bias_bf16 ? 1 : 2;
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(bias), 0, EPI != CGPT_EPI_NONE ? N << bshift : 0, kBufferRsrcWord3);
+  auto load_bias = [&](int i) {
+    int tm, tn;
+    tile_of(min(i, n_mine - 1), tm, tn);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = tn * BN + wn0 + j * 16 + 4 * fgrp;
+      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rb, min(n, N - 4) << bshift, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) braw[j][r] = v[r];
+    }
+  };
+  auto bias_at = [&](int j, int r) -> float {
+    if (!bias_bf16) return __uint_as_float(braw[j][r]);
+    const uint32_t w = braw[j][r >> 1];
+    return __uint_as_float((r & 1) ? (w & 0xffff0000u) : (w << 16));
+  };
+  auto epilogue = [&](int i) {
+    int tm, tn;
+    tile_of(i, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int rows = min(BM, M - m0);
+    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+        C + static_cast<int64_t>(m0) * ldc, 0,
+        static_cast<int>(static_cast<int64_t>(rows) * ldc * static_cast<int64_t>(sizeof(TOut))),
+        kBufferRsrcWord3);
+#pragma unroll
+    for (int ii = 0; ii < TM; ++ii) {
+      const uint32_t roff = static_cast<uint32_t>((wm0 + ii * 16 + frow) * ldc);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = n0 + wn0 + j * 16 + 4 * fgrp;
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float t = acc[ii][j][r];
+          if (EPI != CGPT_EPI_NONE) t += bias_at(j, r);
+          if (EPI == CGPT_EPI_BIAS_GELU) t = gelu_tanh(t);
+          v[r] = t;
+        }
+        const uint32_t off =
+            n < N ? (roff + static_cast<uint32_t>(n)) * static_cast<uint32_t>(sizeof(TOut)) : 0x80000000u;
+        buffer_store4(rc, off, v, static_cast<TOut*>(nullptr));
+      }
+    }
+  };
+
+  // Memory operations an epilogue leaves in flight: its stores and the next
+  // tile's bias loads (capped to the counter's range: a stronger wait).
+  constexpr int EPI_OPS = vm_cap(TM * TN + (EPI != CGPT_EPI_NONE ? TN : 0));
+  Frag f0, f1;
+  if (EPI != CGPT_EPI_NONE) load_bias(0);
+  set_offsets(0);
+  issue(smem);
+  if (total > 1) {
+    issue(smem + STAGE);
+    wait_vmcnt<A_INS + W_INS>();
+  } else {
+    wait_vmcnt<0>();
+  }
+  raw_barrier();
+  read_slab(smem, xo0, f0);
+  int g = 0;
+  for (int t = 0; t < n_mine; ++t) {
+    zero_acc();
+    for (int kt = 0; kt < KT; ++kt, ++g) {
+      uint8_t* cur = smem + (g & 1) * STAGE;
+      read_slab(cur, xo1, f1);
+      mma_slab(f0);
+      if (g + 1 < total) {
+        if (kt == 0 && t > 0)
+          wait_vmcnt<EPI_OPS>();
+        else
+          wait_vmcnt<0>();
+        raw_barrier();
+        if (g + 2 < total) issue(cur);
+        // At a tile's last step the next slab is read after the epilogue,
+        // so its fragments are not live across it.
+        if (kt + 1 < KT) read_slab(smem + ((g + 1) & 1) * STAGE, xo0, f0);
+      }
+      mma_slab(f1);
+    }
+    epilogue(t);
+    if (EPI != CGPT_EPI_NONE) load_bias(t + 1);
+    if (g < total) read_slab(smem + (g & 1) * STAGE, xo0, f0);
   }
 #endif  // __HIP_DEVICE_COMPILE__
 }
@@ -876,9 +1062,10 @@ static const TileCfg kBf16Tiles[] = {
     {256, 128, 4, 2},  // 11: 8 waves (64x64), SPS 1, 6 stages, 144 KiB
     {256, 256, 2, 4},  // 12: 8 waves (128x64), A 3 buffers / W 2, 160 KiB
     {256, 192, 2, 4},  // 13: 8 waves (128x48), A 3 buffers / W 2, 144 KiB
+    {256, 192, 2, 4},  // 14: 8 waves (128x48), fragment reads one slab ahead, 112 KiB
 };
 constexpr int kFirstPipeTile = 5;
-static const int kPipeSps[] = {2, 1, 2, 2, 2, 2, 1, 2, 2};
+static const int kPipeSps[] = {2, 1, 2, 2, 2, 2, 1, 2, 2, 2};
 // fp32 configurations (index = tile id for CGPT_F32).
 static const TileCfg kF32Tiles[] = {
     {128, 128, 2, 2},  // 0
@@ -970,6 +1157,30 @@ static int launch_pipe_a3(const void* a, const void* w, const void* bias, bool b
   return hip_status(hipGetLastError());
 }
 
+// Slab-pipelined kernel (buffer-resource stores only; other output layouts
+// take the two-stage pipeline kernel of the same tile).
+template <int BM, int BN, int WGM, int WGN, int EPI, typename TOut>
+static int launch_slab(const void* a, const void* w, const void* bias, bool bias_bf16, void* c,
+                       int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc, bool vec_store,
+                       hipStream_t s) {
+  static_assert(2 * (BM + BN) * 128 <= 160 * 1024, "LDS budget of one CU");
+  const bool buf_store = vec_store && N % 4 == 0 &&
+                         static_cast<int64_t>(BM) * ldc * static_cast<int64_t>(sizeof(TOut)) < 0x7fffffff;
+  if (!buf_store)
+    return launch_pipe<BM, BN, WGM, WGN, 2, 2, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda,
+                                                          ldw, ldc, vec_store, s);
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = (N + BN - 1) / BN;
+  const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
+  if (tiles > 0x7fffffff) return CGPT_ESHAPE;
+  const int grid = static_cast<int>(tiles < num_cus() ? tiles : num_cus());
+  hipLaunchKernelGGL((gemm_slab_kernel<BM, BN, WGM, WGN, EPI, TOut>), dim3(grid),
+                     dim3(64 * WGM * WGN), 0, s, static_cast<const bf16_t*>(a),
+                     static_cast<const bf16_t*>(w), bias, bias_bf16, static_cast<TOut*>(c), M, N,
+                     K, lda, ldw, ldc, tiles_m, tiles_n, vec_store);
+  return hip_status(hipGetLastError());
+}
+
 // The pipelined kernels address A and W through 32-bit buffer offsets and
 // consume K in whole stages.
 static bool pipe_ok(int tile, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) {
@@ -1009,7 +1220,9 @@ static int launch_tile(int tile, const void* a, const void* w, const void* bias,
       case 13:
         return launch_pipe_a3<256, 192, 2, 4, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda,
                                                          ldw, ldc, vec_store, s);
-
+      case 14:
+        return launch_slab<256, 192, 2, 4, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda, ldw,
+                                                      ldc, vec_store, s);
       default: return CGPT_EINVAL;
     }
   } else {

@@ -18,6 +18,9 @@ Tile ids index the configuration table compiled into libcgpt.so
     bf16, the same pipeline with A fetched two steps ahead (3 A buffers,
     2 W buffers, 2 k32 slabs per stage; buffer-store outputs only):
           12 = 256x256                             13 = 256x192
+    bf16, 2 stages of 2 slabs with each slab's fragment reads issued while the
+    previous slab's MFMAs run (buffer-store outputs only):
+          14 = 256x192 (8 waves of 128x48)
     fp32: 0 = 128x128, 1 = 64x64
 
 ``TABLE`` maps exact (dtype, M, N, K) problems measured on MI355X to the tile
@@ -36,10 +39,10 @@ from . import _lib
 _B = _lib.CGPT_BF16
 TABLE: Dict[Tuple[int, int, int, int], int] = {
     # GPT-2 124M prefill, M = 16 x 1024
-    (_B, 16384, 2304, 768): 7,    # c_attn       797
-    (_B, 16384, 768, 768): 7,     # attn c_proj  741
-    (_B, 16384, 3072, 768): 12,   # c_fc         901
-    (_B, 16384, 768, 3072): 7,    # mlp c_proj  1147
+    (_B, 16384, 2304, 768): 14,   # c_attn       824
+    (_B, 16384, 768, 768): 14,    # attn c_proj  752
+    (_B, 16384, 3072, 768): 12,   # c_fc         865
+    (_B, 16384, 768, 3072): 14,   # mlp c_proj  1160
     (_B, 16384, 50304, 768): 12,  # lm head (vocab padded), fp32 out 809
     # 'medium' (8L, d 512) prefill, M = 16 x 256
     (_B, 4096, 1536, 512): 10,    # 420
