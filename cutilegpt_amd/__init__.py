@@ -25,6 +25,7 @@ from .kernels import (  # noqa: F401
 )
 from .model import CutileGPT  # noqa: F401
 from .hf_loader import HFWeightLoader  # noqa: F401
+from . import api  # noqa: F401  (Tile API: cutilegpt_amd.api.tile, configure_tiles, ...)
 
 __all__ = [
     "__version__",
