@@ -308,6 +308,9 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
 }
 
+// s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt at their maxima).
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
 // Wait until the stage that has `later` stages of LPS loads each issued after
 // it, plus (when `stores`) ST stores, has landed: vmcnt retires loads and
 // stores in issue order.  Counts past the 6-bit counter's range wait for 63
@@ -850,7 +853,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_a3_kernel(
 //            read slab 0 of stage g+1    | MFMAs of slab 1 of stage g
 //            [last step of a tile: epilogue, next tile's bias]
 // The barrier sits between the two slabs: once every wave has read all of
-// stage g its buffer can be refilled.  Buffer-resource stores only.
+// stage g its buffer can be refilled.  Output rows are staged through LDS and
+// stored as whole lines (requires 16-byte aligned rows and N a multiple of
+// 16 bytes' worth of elements).
 template <int BM, int BN, int WGM, int WGN, int EPI, typename TOut>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_slab_kernel(
     const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, const void* __restrict__ bias,
@@ -864,7 +869,21 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_slab_kernel(
   constexpr int STAGE = (BM + BN) * ROWB;
   constexpr int A_INS = BM / (RPI * NW), W_INS = BN / (RPI * NW);
   static_assert(BM % (RPI * NW) == 0 && BN % (RPI * NW) == 0, "tile/wave mismatch");
+  // Output staging: the rest of the CU's LDS holds IIP 16-row bands of every
+  // wave row (PASS_ROWS rows of the tile), written in the MFMA layout and read
+  // back as consecutive 16-byte chunks of whole rows.
+  constexpr int OUT_BYTES = 160 * 1024 - 2 * STAGE;
+  constexpr int ROWB_O = BN * static_cast<int>(sizeof(TOut));  // bytes of one tile row
+  constexpr int CPRO = ROWB_O / 16;                            // 16-byte chunks per row
+  constexpr int IIP = OUT_BYTES / (WGM * 16 * ROWB_O);
+  constexpr int PASS_ROWS = WGM * 16 * IIP;
+  constexpr int CH_PER_T = PASS_ROWS * CPRO / NT;
+  constexpr int NPASS = TM / IIP;
+  static_assert(IIP >= 1 && TM % IIP == 0, "output staging bands");
+  static_assert(PASS_ROWS * CPRO == CH_PER_T * NT, "whole chunks per thread");
+  static_assert(CPRO % 8 == 0, "rows of whole 128-byte groups");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t sout[OUT_BYTES];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
@@ -884,23 +903,40 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_slab_kernel(
   };
 
   // ---- issue side (flat stage stream over this block's tiles)
-  int iss_i = 0, iss_kt = 0;
+  // Per-lane source offsets are set once and moved by a uniform delta at each
+  // tile change.  Rows past M (or N) are not clamped: their offsets lie past
+  // the resource's size, so the hardware returns zeros for them (such rows
+  // are never stored); the launcher checks that these offsets fit 32 bits.
+  int iss_i = 0, iss_kt = 0, iss_tm = 0, iss_tn = 0;
   uint32_t aoff[A_INS], woff[W_INS];
-  auto set_offsets = [&](int i) {
-    int tm, tn;
-    tile_of(i, tm, tn);
+  {
+    tile_of(0, iss_tm, iss_tn);
 #pragma unroll
     for (int ii = 0; ii < A_INS; ++ii) {
       const int row = (ii * NW + wave) * RPI + lrow;
-      const int64_t g = min(tm * BM + row, M - 1);
-      aoff[ii] = static_cast<uint32_t>(g * lda * 2 + ((pchunk ^ (row & 7)) << 4));
+      aoff[ii] = static_cast<uint32_t>(static_cast<int64_t>(iss_tm * BM + row) * lda * 2 +
+                                       ((pchunk ^ (row & 7)) << 4));
     }
 #pragma unroll
     for (int ii = 0; ii < W_INS; ++ii) {
       const int row = (ii * NW + wave) * RPI + lrow;
-      const int64_t g = min(tn * BN + row, N - 1);
-      woff[ii] = static_cast<uint32_t>(g * ldw * 2 + ((pchunk ^ (row & 7)) << 4));
+      woff[ii] = static_cast<uint32_t>(static_cast<int64_t>(iss_tn * BN + row) * ldw * 2 +
+                                       ((pchunk ^ (row & 7)) << 4));
     }
+  }
+  const uint32_t a_tile_bytes = static_cast<uint32_t>(BM * lda * 2);
+  const uint32_t w_tile_bytes = static_cast<uint32_t>(BN * ldw * 2);
+  auto set_offsets = [&](int i) {
+    int tm, tn;
+    tile_of(i, tm, tn);
+    const uint32_t da = static_cast<uint32_t>(tm - iss_tm) * a_tile_bytes;
+    const uint32_t dw = static_cast<uint32_t>(tn - iss_tn) * w_tile_bytes;
+    iss_tm = tm;
+    iss_tn = tn;
+#pragma unroll
+    for (int ii = 0; ii < A_INS; ++ii) aoff[ii] += da;
+#pragma unroll
+    for (int ii = 0; ii < W_INS; ++ii) woff[ii] += dw;
   };
   auto issue = [&](uint8_t* buf) {
     const int soff = iss_kt * ROWB;
@@ -964,6 +1000,16 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_slab_kernel(
     const uint32_t w = braw[j][r >> 1];
     return __uint_as_float((r & 1) ? (w & 0xffff0000u) : (w << 16));
   };
+  // Epilogue through LDS: each pass writes IIP row bands of every wave (bias
+  // and GELU applied) into sout, barrier, then every thread stores CH_PER_T
+  // consecutive 16-byte chunks of whole tile rows, so a wave's store covers
+  // full 128-byte lines (the MFMA layout would give 16 rows x 32 or 64 bytes
+  // per store).  16-byte chunk c of staged row r sits at slot c ^ (r & 7)
+  // within its 128-byte group (conflict-free column writes and row reads).
+  // Exactly NPASS * CH_PER_T stores per thread: rows past M fall outside the
+  // resource, chunks past N get an offset past it.
+  auto spos = [](int r, int c) { return r * ROWB_O + (((c & ~7) | ((c & 7) ^ (r & 7))) << 4); };
+  const int wr = wave / WGN;
   auto epilogue = [&](int i) {
     int tm, tn;
     tile_of(i, tm, tn);
@@ -973,33 +1019,66 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_slab_kernel(
         C + static_cast<int64_t>(m0) * ldc, 0,
         static_cast<int>(static_cast<int64_t>(rows) * ldc * static_cast<int64_t>(sizeof(TOut))),
         kBufferRsrcWord3);
+    // An opaque zero defined here keeps the per-lane staging and store
+    // addresses from being hoisted out of the tile loop, where they would
+    // stay live (and spill) through every K step.
+    int zero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+    const int lt = tid + zero, lrw = frow + zero;
 #pragma unroll
-    for (int ii = 0; ii < TM; ++ii) {
-      const uint32_t roff = static_cast<uint32_t>((wm0 + ii * 16 + frow) * ldc);
+    for (int p = 0; p < NPASS; ++p) {
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int n = n0 + wn0 + j * 16 + 4 * fgrp;
-        float v[4];
+      for (int il = 0; il < IIP; ++il) {
+        const int ii = p * IIP + il;
+        const int r = (wr * IIP + il) * 16 + lrw;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float t = acc[ii][j][r];
-          if (EPI != CGPT_EPI_NONE) t += bias_at(j, r);
-          if (EPI == CGPT_EPI_BIAS_GELU) t = gelu_tanh(t);
-          v[r] = t;
+        for (int j = 0; j < TN; ++j) {
+          float v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float t = acc[ii][j][q];
+            if (EPI != CGPT_EPI_NONE) t += bias_at(j, q);
+            if (EPI == CGPT_EPI_BIAS_GELU) t = gelu_tanh(t);
+            v[q] = t;
+          }
+          const int byte = (wn0 + j * 16 + 4 * fgrp) * static_cast<int>(sizeof(TOut));
+          uint8_t* dst = sout + spos(r, byte >> 4) + (byte & 15);
+          if constexpr (sizeof(TOut) == 4) {
+            *reinterpret_cast<u32x4_t*>(dst) = u32x4_t{__float_as_uint(v[0]), __float_as_uint(v[1]),
+                                                       __float_as_uint(v[2]), __float_as_uint(v[3])};
+          } else {
+            *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+          }
         }
-        const uint32_t off =
-            n < N ? (roff + static_cast<uint32_t>(n)) * static_cast<uint32_t>(sizeof(TOut)) : 0x80000000u;
-        buffer_store4(rc, off, v, static_cast<TOut*>(nullptr));
+      }
+      wait_lgkm0();
+      raw_barrier();
+#pragma unroll
+      for (int q = 0; q < CH_PER_T; ++q) {
+        const int ch = lt + q * NT;
+        const int r = ch / CPRO, c = ch % CPRO;
+        const u32x4_t d = *reinterpret_cast<const u32x4_t*>(sout + spos(r, c));
+        // Staged row r: wave row r / (16 IIP), band p * IIP + (r / 16) % IIP.
+        const int grow = (r / (16 * IIP)) * WM + p * IIP * 16 + r % (16 * IIP);
+        const int ncol = n0 + c * (16 / static_cast<int>(sizeof(TOut)));
+        const uint32_t off = ncol < N ? static_cast<uint32_t>(
+                                            (static_cast<int64_t>(grow) * ldc + ncol) * sizeof(TOut))
+                                      : 0x80000000u;
+        __builtin_amdgcn_raw_buffer_store_b128(d, rc, off, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (p + 1 < NPASS) {
+        wait_lgkm0();
+        raw_barrier();
       }
     }
   };
 
   // Memory operations an epilogue leaves in flight: its stores and the next
   // tile's bias loads (capped to the counter's range: a stronger wait).
-  constexpr int EPI_OPS = vm_cap(TM * TN + (EPI != CGPT_EPI_NONE ? TN : 0));
+  constexpr int EPI_OPS = vm_cap(NPASS * CH_PER_T + (EPI != CGPT_EPI_NONE ? TN : 0));
   Frag f0, f1;
   if (EPI != CGPT_EPI_NONE) load_bias(0);
-  set_offsets(0);
   issue(smem);
   if (total > 1) {
     issue(smem + STAGE);
@@ -1157,14 +1236,26 @@ static int launch_pipe_a3(const void* a, const void* w, const void* bias, bool b
   return hip_status(hipGetLastError());
 }
 
-// Slab-pipelined kernel (buffer-resource stores only; other output layouts
-// take the two-stage pipeline kernel of the same tile).
+// Slab-pipelined kernel (whole-line staged stores only; other output layouts
+// take the two-stage pipeline kernel of the same tile).  Its source offsets
+// are not clamped to the last row, so a whole tile past M (or N) must still
+// address below 4 GiB.
 template <int BM, int BN, int WGM, int WGN, int EPI, typename TOut>
 static int launch_slab(const void* a, const void* w, const void* bias, bool bias_bf16, void* c,
                        int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc, bool vec_store,
                        hipStream_t s) {
-  static_assert(2 * (BM + BN) * 128 <= 160 * 1024, "LDS budget of one CU");
-  const bool buf_store = vec_store && N % 4 == 0 &&
+  if ((static_cast<int64_t>(M) + BM) * lda * 2 >= (int64_t{1} << 32) ||
+      (static_cast<int64_t>(N) + BN) * ldw * 2 >= (int64_t{1} << 32) ||
+      static_cast<int64_t>(BM) * lda * 2 >= (int64_t{1} << 31) ||
+      static_cast<int64_t>(BN) * ldw * 2 >= (int64_t{1} << 31))
+    return launch_pipe<BM, BN, WGM, WGN, 2, 2, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda,
+                                                          ldw, ldc, vec_store, s);
+  static_assert(2 * (BM + BN) * 128 < 160 * 1024, "LDS budget of one CU");
+  // Whole 16-byte chunks: N and ldc multiples of 16 bytes' worth of elements
+  // and a 16-byte aligned C (vec_store guarantees only 8 bytes for bf16).
+  constexpr int EPC = 16 / static_cast<int>(sizeof(TOut));
+  const bool buf_store = vec_store && N % EPC == 0 && ldc % EPC == 0 &&
+                         reinterpret_cast<uintptr_t>(c) % 16 == 0 &&
                          static_cast<int64_t>(BM) * ldc * static_cast<int64_t>(sizeof(TOut)) < 0x7fffffff;
   if (!buf_store)
     return launch_pipe<BM, BN, WGM, WGN, 2, 2, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda,

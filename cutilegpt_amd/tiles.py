@@ -19,7 +19,8 @@ Tile ids index the configuration table compiled into libcgpt.so
     2 W buffers, 2 k32 slabs per stage; buffer-store outputs only):
           12 = 256x256                             13 = 256x192
     bf16, 2 stages of 2 slabs with each slab's fragment reads issued while the
-    previous slab's MFMAs run (buffer-store outputs only):
+    previous slab's MFMAs run, output rows staged through LDS and stored as
+    whole lines (rows of 16-byte multiples; otherwise the 2-stage kernel):
           14 = 256x192 (8 waves of 128x48)
     fp32: 0 = 128x128, 1 = 64x64
 
@@ -39,14 +40,14 @@ from . import _lib
 _B = _lib.CGPT_BF16
 TABLE: Dict[Tuple[int, int, int, int], int] = {
     # GPT-2 124M prefill, M = 16 x 1024
-    (_B, 16384, 2304, 768): 14,   # c_attn       824
-    (_B, 16384, 768, 768): 14,    # attn c_proj  752
-    (_B, 16384, 3072, 768): 12,   # c_fc         865
-    (_B, 16384, 768, 3072): 14,   # mlp c_proj  1160
+    (_B, 16384, 2304, 768): 14,   # c_attn       981
+    (_B, 16384, 768, 768): 14,    # attn c_proj  841
+    (_B, 16384, 3072, 768): 12,   # c_fc         865 (GELU epilogue: 12 is faster in the model)
+    (_B, 16384, 768, 3072): 14,   # mlp c_proj  1202
     (_B, 16384, 50304, 768): 12,  # lm head (vocab padded), fp32 out 809
     # 'medium' (8L, d 512) prefill, M = 16 x 256
-    (_B, 4096, 1536, 512): 10,    # 420
-    (_B, 4096, 2048, 512): 10,    # 532
+    (_B, 4096, 1536, 512): 14,    # 431
+    (_B, 4096, 2048, 512): 14,    # 533
     (_B, 4096, 512, 2048): 3,     # 271
     (_B, 4096, 50304, 512): 5,    # lm head (vocab padded), fp32 out 666
 }
