@@ -345,9 +345,288 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
   }
 }
 
+// bf16 variant with K and V streamed straight into LDS (head_dim 64 or 128).
+// Differences from attn_fwd_kernel:
+//  * Keys and values go global -> LDS by buffer_load ... lds (no staging
+//    registers, no LDS writes), STAGES blocks deep: block j + STAGES - 1 is
+//    issued at step j into the buffer block j - 1 has released.  As in the
+//    GEMM pipeline these loads are invisible to the compiler, so each step
+//    ends with an explicit s_waitcnt for this wave's part of block j + 1 and
+//    starts with a barrier.
+//  * V stays row-major ([key][d], like K) and the V^T operand of O^T = V^T P^T
+//    is read with ds_read_b64_tr_b16: within a 16-lane group, lane k points at
+//    4 consecutive d of key (4j + k/4)-th row and receives, transposed, the 4
+//    keys of its own d.  Two such reads give the 8-key k-slab in the key order
+//    of the P operand (keys 32c + 4g + r, then 32c + 16 + 4g + r).
+//  * 16-byte chunk c of row r is stored at chunk c ^ (r & 7): the DMA lane
+//    that fills a slot fetches the chunk that belongs there.
+template <int HD, int STAGES>
+__global__ __launch_bounds__(kAttnThreads) void attn_fwd_dma_kernel(
+    const bf16_t* __restrict__ Q, const bf16_t* __restrict__ K, const bf16_t* __restrict__ V,
+    bf16_t* __restrict__ O, int H, int Tq, int Tk, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    int64_t o_sb, int64_t o_sh, int64_t o_st, float scale_log2, int causal, int n_bh) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int QT = kAttnQT, BQ = kAttnBQ, BKV = kAttnBKV;
+  constexpr int NWAVE = kAttnThreads / 64;
+  constexpr int KROW = HD * 2;                 // bytes per K / V row
+  constexpr int CPR = KROW / 16;               // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;                // rows per 1 KiB DMA instruction
+  constexpr int XB = BKV * KROW;               // bytes of K (or V) per block
+  constexpr int INS = XB / 1024 / NWAVE;       // DMA instructions per wave per operand
+  constexpr int LPS = 2 * INS;
+  constexpr int STAGE = 2 * XB;
+  constexpr int NKS = HD / 32;                 // k32 slabs of head_dim
+  constexpr int ND = HD / 16;
+  static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
+  static_assert(INS * NWAVE * 1024 == XB, "whole DMA instructions per wave");
+  static_assert((STAGES - 2) * LPS < 64, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, frow = lane & 15;
+
+  const int n_qblk = (Tq + BQ - 1) / BQ;
+  const int qb = n_qblk - 1 - static_cast<int>(blockIdx.x) / n_bh;  // heavy blocks first
+  const int bh = static_cast<int>(blockIdx.x) % n_bh;
+  const int b = bh / H, h = bh % H;
+  const int q0 = qb * BQ;
+  const int off = Tk - Tq;
+
+  const bf16_t* Qb = Q + b * q_sb + h * q_sh;
+  const u32x4_t rk = buffer_desc(K + b * k_sb + h * k_sh,
+                                 static_cast<uint32_t>((static_cast<int64_t>(Tk - 1) * k_st + HD) * 2));
+  const u32x4_t rv = buffer_desc(V + b * v_sb + h * v_sh,
+                                 static_cast<uint32_t>((static_cast<int64_t>(Tk - 1) * v_st + HD) * 2));
+
+  u32x4_t qf[QT][NKS];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int qi = q0 + wave * 16 * QT + qt * 16 + frow;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks)
+      qf[qt][ks] = qi < Tq ? *reinterpret_cast<const u32x4_t*>(Qb + qi * q_st + (4 * ks + g) * 8)
+                           : u32x4_t{0, 0, 0, 0};
+  }
+  // Retire the Q loads here: left to the compiler, the wait would sit before
+  // the first MFMA inside the key loop and drain the DMA queue every block.
+  wait_vmcnt<0>();
+
+  const int last_q = min(q0 + BQ, Tq) - 1 + off;
+  const int kv_end = causal ? min(last_q + 1, Tk) : Tk;
+  const int n_kv = (kv_end + BKV - 1) / BKV;
+  const int wave_q0 = q0 + wave * 16 * QT;
+  const int wave_last = min(wave_q0 + 16 * QT, Tq) - 1 + off;
+  const bool wave_live = wave_q0 < Tq;
+
+  // DMA of block j into stage buffer `buf`: instruction ii of this wave
+  // fills rows (ii * NWAVE + wave) * RPI + lane / CPR; keys past Tk re-read
+  // the last key (masked later).
+  const int lrow = lane / CPR, slot = lane % CPR;
+  auto issue = [&](int j, uint8_t* buf) {
+    const int kv0 = j * BKV;
+#pragma unroll
+    for (int ii = 0; ii < INS; ++ii) {
+      const int row = (ii * NWAVE + wave) * RPI + lrow;
+      const int key = min(kv0 + row, Tk - 1);
+      const uint32_t chunk = static_cast<uint32_t>((slot ^ (row & 7)) << 4);
+      const uint32_t lds = (ii * NWAVE + wave) * 1024;
+      dma_lds16(rk, lds_addr(buf + lds), static_cast<uint32_t>(key * k_st * 2) + chunk, 0);
+      dma_lds16(rv, lds_addr(buf + XB + lds), static_cast<uint32_t>(key * v_st * 2) + chunk, 0);
+    }
+  };
+  // This wave's part of the block `later` stages before the newest one has
+  // landed (and its LDS reads are done).
+  auto wait_later = [&](int later) {
+    if constexpr (STAGES >= 3)
+      if (later >= 1) {
+        wait_vmcnt<LPS>();
+        return;
+      }
+    wait_vmcnt<0>();
+  };
+
+  f32x4_t o_acc[QT][ND];
+  float m_run[QT], l_run[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    m_run[qt] = -INFINITY;
+    l_run[qt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) o_acc[qt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // V^T read: lane (g, k) of the 16-lane group points at row 4g + k/4 (plus
+  // the slab's base key) and d = dt*16 + 4 (k % 4).
+  const int tr_row = 4 * g + (frow >> 2);
+  const int tr_byte = 8 * (frow & 3);
+  auto vt_read = [&](const uint8_t* sv, int row, int dt) -> u32x2_t {
+    const int byte = dt * 32 + tr_byte;
+    const uint8_t* p = sv + row * KROW + ((((byte >> 4) ^ (row & 7))) << 4) + (byte & 15);
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)((__attribute__((address_space(3))) uint8_t*)(p)));
+    return __builtin_bit_cast(u32x2_t, r);
+  };
+
+  int ib = 0;
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < n_kv) {
+      issue(s, smem + s * STAGE);
+      ib = s + 1;
+    }
+  if (n_kv > 0) wait_later(n_kv - 1 > STAGES - 2 ? STAGES - 2 : n_kv - 1);
+  int cb = 0;
+  for (int j = 0; j < n_kv; ++j) {
+    raw_barrier();
+    if (j + STAGES - 1 < n_kv) {
+      issue(j + STAGES - 1, smem + ib * STAGE);
+      ib = ib + 1 == STAGES ? 0 : ib + 1;
+    }
+    const int kv0 = j * BKV;
+    const uint8_t* sk = smem + cb * STAGE;
+    const uint8_t* sv = sk + XB;
+    cb = cb + 1 == STAGES ? 0 : cb + 1;
+    if (wave_live && !(causal && kv0 > wave_last)) {
+      f32x4_t s[QT][4];
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) s[qt][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        const int c = 4 * ks + g;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+          const int key = kt * 16 + frow;
+          const u32x4_t kf =
+              *reinterpret_cast<const u32x4_t*>(sk + key * KROW + ((c ^ (key & 7)) << 4));
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) AttnMfma<bf16_t>::run(kf, qf[qt][ks], s[qt][kt]);
+        }
+      }
+      constexpr float kLazyLog2 = 8.0f;
+      const bool need_mask = (causal && kv0 + BKV - 1 > wave_q0 + off) || (kv0 + BKV > Tk);
+      if (need_mask) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          const int qpos = wave_q0 + qt * 16 + frow + off;
+          const int lim = (causal ? min(qpos, Tk - 1) : Tk - 1) - kv0 - 4 * g;
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              s[qt][kt][r] = (kt * 16 + r > lim) ? -INFINITY : s[qt][kt][r];
+        }
+      }
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, s[qt][kt][r]);
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        const float mblk = mloc * scale_log2;
+        const bool grow = mblk > m_run[qt] + kLazyLog2;
+        if (__any(grow)) {
+          const float m_new = grow ? mblk : m_run[qt];
+          const float alpha = grow ? __builtin_amdgcn_exp2f(m_run[qt] - m_new) : 1.0f;
+          m_run[qt] = m_new;
+          l_run[qt] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o_acc[qt][dt][r] *= alpha;
+        }
+        const float neg_m = m_run[qt] == -INFINITY ? 0.f : -m_run[qt];
+        float lsum = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qt][kt][r], scale_log2, neg_m));
+            s[qt][kt][r] = p;
+            lsum += p;
+          }
+        l_run[qt] += lsum;
+      }
+      // O^T += V^T P^T, k-slab c = keys 32c .. 32c + 31.
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        u32x4_t pf[QT];
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+          pf[qt] = u32x4_t{pack_bf16x2(s[qt][2 * c][0], s[qt][2 * c][1]),
+                           pack_bf16x2(s[qt][2 * c][2], s[qt][2 * c][3]),
+                           pack_bf16x2(s[qt][2 * c + 1][0], s[qt][2 * c + 1][1]),
+                           pack_bf16x2(s[qt][2 * c + 1][2], s[qt][2 * c + 1][3])};
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt) {
+          const u32x2_t lo = vt_read(sv, 32 * c + tr_row, dt);
+          const u32x2_t hi = vt_read(sv, 32 * c + 16 + tr_row, dt);
+          const u32x4_t vf = {lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) AttnMfma<bf16_t>::run(vf, pf[qt], o_acc[qt][dt]);
+        }
+      }
+    }
+    if (j + 1 < n_kv) wait_later(n_kv - 1 - (j + 1) > STAGES - 2 ? STAGES - 2 : n_kv - 1 - (j + 1));
+  }
+
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int qi = wave_q0 + qt * 16 + frow;
+    float l = l_run[qt];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    if (qi >= Tq) continue;
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    bf16_t* orow = O + b * o_sb + h * o_sh + qi * o_st;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) {
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = o_acc[qt][dt][r] * inv;
+      store4_o(orow + dt * 16 + 4 * g, v);
+    }
+  }
+#endif  // __HIP_DEVICE_COMPILE__
+}
+
+// The DMA kernel addresses a (batch, head)'s keys and values through 32-bit
+// buffer offsets.
+static bool attn_dma_ok(int Tk, const int64_t* st) {
+  return (static_cast<int64_t>(Tk) + 1) * st[5] * 2 < (int64_t{1} << 31) &&
+         (static_cast<int64_t>(Tk) + 1) * st[8] * 2 < (int64_t{1} << 31);
+}
+
+template <int HD, int STAGES>
+static int launch_attn_dma(const void* q, const void* k, const void* v, void* o, int B, int H,
+                           int Tq, int Tk, const int64_t* st, float scale, int causal,
+                           hipStream_t s) {
+  const int n_bh = B * H;
+  const int n_qblk = (Tq + kAttnBQ - 1) / kAttnBQ;
+  const int64_t blocks = static_cast<int64_t>(n_bh) * n_qblk;
+  if (blocks > 0x7fffffff) return CGPT_ESHAPE;
+  const float scale_log2 = scale * 1.4426950408889634f;
+  hipLaunchKernelGGL((attn_fwd_dma_kernel<HD, STAGES>), dim3(static_cast<unsigned>(blocks)),
+                     dim3(kAttnThreads), 0, s, static_cast<const bf16_t*>(q),
+                     static_cast<const bf16_t*>(k), static_cast<const bf16_t*>(v),
+                     static_cast<bf16_t*>(o), H, Tq, Tk, st[0], st[1], st[2], st[3], st[4], st[5],
+                     st[6], st[7], st[8], st[9], st[10], st[11], scale_log2, causal, n_bh);
+  return hip_status(hipGetLastError());
+}
+
 template <typename T, int HD>
 static int launch_attn(const void* q, const void* k, const void* v, void* o, int B, int H, int Tq,
                        int Tk, const int64_t* st, float scale, int causal, hipStream_t s) {
+  if constexpr (sizeof(T) == 2 && (HD == 64 || HD == 128)) {
+    if (attn_dma_ok(Tk, st))
+      return launch_attn_dma<HD, HD == 64 ? 3 : 2>(q, k, v, o, B, H, Tq, Tk, st, scale, causal, s);
+  }
   const int n_bh = B * H;
   const int n_qblk = (Tq + kAttnBQ - 1) / kAttnBQ;
   const int64_t blocks = static_cast<int64_t>(n_bh) * n_qblk;

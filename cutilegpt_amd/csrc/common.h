@@ -127,6 +127,49 @@ __device__ __forceinline__ void store4_out(bf16_t* p, const float* v) {
 }
 
 
+// ---- direct-to-LDS streaming (shared by the GEMM and attention pipelines)
+
+#if defined(__HIP_DEVICE_COMPILE__)
+// Raw buffer descriptor (base, no stride, `bytes` records, gfx9 raw format).
+__device__ __forceinline__ u32x4_t buffer_desc(const void* p, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  return u32x4_t{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32) & 0xffffu, bytes,
+                 0x00020000u};
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint8_t*)(p)));
+}
+// Global -> LDS DMA of 16 bytes per lane: lane l's bytes land at M0 + 16 l.
+// Issued from inline assembly on purpose: the compiler then
+// neither counts these loads nor guards later LDS reads against them, so the
+// stage pipeline's own vmcnt waits and barriers are the only synchronisation
+// (the compiler cannot prove that a read of one stage buffer does not alias
+// the DMA into another and would otherwise drain the queue before every
+// read).  M0 needs one wait state after its write.
+__device__ __forceinline__ void dma_lds16(u32x4_t desc, uint32_t lds, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(lds), "v"(voff), "s"(desc), "s"(soff) : "memory", "m0");
+}
+#endif
+
+__device__ __forceinline__ void raw_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt[3:0], expcnt[6:4],
+// lgkmcnt[11:8], vmcnt[5:4] at [15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
+}
+
+// s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt at their maxima).
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
 // Error codes shared with the C ABI (see include/cgpt.h).
 __host__ __forceinline__ int hip_status(hipError_t e) {
   return e == hipSuccess ? CGPT_OK : static_cast<int>(e);
