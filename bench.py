@@ -214,7 +214,7 @@ def main():
         "config": {"workload": wl["name"], "n_layer": L, "n_head": H, "n_embd": D,
                    "vocab_size": V, "batch": B, "seq_len": T, "logits": "fp32",
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "kernel": "lm_head GEMM (gemm_pipe_a3_kernel 256x256, bf16 in, fp32 out, N=50257 padded to 50304, K=768)",
+        "roofline": {"bound": "mfma", "kernel": "lm_head GEMM (gemm_pipe_kernel 256x256, wave-staged whole-line stores, bf16 in, fp32 out, N=50257 padded to 50304, K=768)",
                      "achieved": round(head_tflops, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(head_tflops / PEAK_BF16_TFLOPS, 4),
                      "traffic": LM_HEAD_TRAFFIC_BYTES if args.workload == "gpt2" else None,

@@ -295,10 +295,16 @@ __device__ __forceinline__ void wait_stages(int later, bool stores) {
 
 constexpr uint32_t kBufferRsrcWord3 = 0x00020000u;  // raw buffer, gfx9 family
 
+// Output modes of gemm_pipe_kernel.
+constexpr int kOutPlain = 0, kOutBuffer = 1, kOutWaveStaged = 2;
 
-// BUFST: every output store goes through a buffer resource (requires N % 4 == 0
-// and 16/8-byte aligned rows); otherwise plain stores behind per-lane bounds.
-template <int BM, int BN, int WGM, int WGN, int SPS, int STAGES, int EPI, typename TOut, bool BUFST>
+
+// OUTM: kOutBuffer — every output store goes through a buffer resource
+// (requires N % 4 == 0 and 16/8-byte aligned rows); kOutWaveStaged — the same,
+// with each wave's rows staged through LDS so a store writes whole lines
+// (requires rows of 16-byte multiples); kOutPlain — plain stores behind
+// per-lane bounds.
+template <int BM, int BN, int WGM, int WGN, int SPS, int STAGES, int EPI, typename TOut, int OUTM>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
     const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, const void* __restrict__ bias,
     bool bias_bf16, TOut* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldw,
@@ -322,8 +328,17 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
   static_assert((STAGES - 2) * LPS < 64, "vmcnt range");
   // Stage buffers at computed offsets in one array (the DMA writes them
   // through M0, so the compiler sees only the fragment reads).
+  constexpr bool BUFST = OUTM >= kOutBuffer;
+  // Wave-staged output: each wave's 16-row band of its WN columns (bias and
+  // GELU applied) goes through a private LDS slot and out as whole rows.
+  constexpr int WROWB = WN * static_cast<int>(sizeof(TOut));  // bytes of a wave's row
+  constexpr int WCPR = WROWB / 16;                              // 16-byte chunks per row
+  constexpr int WNQ = 16 * WCPR / 64;                           // stores per 16-row band
+  static_assert(OUTM != kOutWaveStaged || (WCPR % 8 == 0 && WNQ * 64 == 16 * WCPR),
+                "wave rows of whole 128-byte lines");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE];
-  __shared__ float escr[NW][kScrFloats];
+  __shared__ float escr[OUTM == kOutPlain ? NW : 1][OUTM == kOutPlain ? kScrFloats : 1];
+  __shared__ __attribute__((aligned(16))) uint8_t sout[OUTM == kOutWaveStaged ? NW * 16 * WROWB : 16];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
@@ -461,7 +476,59 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
     tile_coords(static_cast<int>(blockIdx.x) + i * static_cast<int>(gridDim.x), tiles_m, tiles_n,
                 tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
-    if constexpr (BUFST) {
+    if constexpr (OUTM == kOutWaveStaged) {
+      // Per 16-row band: write the band (16-byte chunk c of row r at slot
+      // c ^ (r & 7) of its 128-byte group), then WNQ stores of 64 consecutive
+      // chunks each, i.e. 64 / WCPR whole rows of the wave's columns.  The
+      // slot is private to the wave (LDS keeps one wave's accesses in order),
+      // so no barrier is needed.  An opaque zero keeps the addresses inside
+      // the tile loop (hoisted, they would stay live through every K step).
+      int zero;
+      asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+      uint8_t* sw = sout + wave * 16 * WROWB;
+      auto spos = [](int r, int c) { return r * WROWB + (((c & ~7) | ((c & 7) ^ (r & 7))) << 4); };
+      const int rows = min(BM, M - m0);
+      const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+          C + static_cast<int64_t>(m0) * ldc, 0,
+          static_cast<int>(static_cast<int64_t>(rows) * ldc * static_cast<int64_t>(sizeof(TOut))),
+          kBufferRsrcWord3);
+      const int lr = frow + zero, ll = lane + zero;
+#pragma unroll
+      for (int ii = 0; ii < TM; ++ii) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float t = acc[ii][j][r];
+            if (EPI != CGPT_EPI_NONE) t += bias_at(j, r, 0);
+            if (EPI == CGPT_EPI_BIAS_GELU) t = gelu_tanh(t);
+            v[r] = t;
+          }
+          const int byte = (j * 16 + 4 * fgrp) * static_cast<int>(sizeof(TOut));
+          uint8_t* dst = sw + spos(lr, byte >> 4) + (byte & 15);
+          if constexpr (sizeof(TOut) == 4) {
+            *reinterpret_cast<u32x4_t*>(dst) = u32x4_t{__float_as_uint(v[0]), __float_as_uint(v[1]),
+                                                       __float_as_uint(v[2]), __float_as_uint(v[3])};
+          } else {
+            *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < WNQ; ++q) {
+          const int ch = q * 64 + ll;
+          const int r = ch / WCPR, c = ch % WCPR;
+          const u32x4_t d = *reinterpret_cast<const u32x4_t*>(sw + spos(r, c));
+          const int col = n0 + wn0 + c * (16 / static_cast<int>(sizeof(TOut)));
+          const uint32_t off =
+              col < N ? static_cast<uint32_t>((static_cast<int64_t>(wm0 + ii * 16 + r) * ldc + col) *
+                                              sizeof(TOut))
+                      : 0x80000000u;
+          __builtin_amdgcn_raw_buffer_store_b128(d, rc, off, 0, 0);
+        }
+      }
+      return true;
+    } else if constexpr (BUFST) {
       const int rows = min(BM, M - m0);
       const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
           C + static_cast<int64_t>(m0) * ldc, 0,
@@ -524,7 +591,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
   Frag fr;
   // Memory operations a buffer-store epilogue issues: its stores and the next
   // tile's bias loads.
-  constexpr int EPI_OPS = TM * TN + (EPI != CGPT_EPI_NONE ? TN : 0);
+  constexpr int EPI_OPS = vm_cap((OUTM == kOutWaveStaged ? TM * WNQ : TM * TN) +
+                                 (EPI != CGPT_EPI_NONE ? TN : 0));
   // Wait until stage `h` has landed: `later` stages issued after it may stay
   // in flight, and so may the exact EPI_OPS operations of a buffer-store
   // epilogue issued after them.
@@ -1100,7 +1168,7 @@ static const TileCfg kBf16Tiles[] = {
     {256, 256, 2, 4},  // 12: 8 waves (128x64), A 3 buffers / W 2, 160 KiB
     {256, 192, 2, 4},  // 13: 8 waves (128x48), A 3 buffers / W 2, 144 KiB
     {256, 192, 2, 4},  // 14: 8 waves (128x48), fragment reads one slab ahead, 112 KiB
-    {256, 256, 2, 4},  // 15: 8 waves (128x64), fragment reads one slab ahead, 128 KiB
+    {256, 256, 2, 4},  // 15: 8 waves (128x64), SPS 2, 2 stages, rows staged per wave, 160 KiB
 };
 constexpr int kFirstPipeTile = 5;
 static const int kPipeSps[] = {2, 1, 2, 2, 2, 2, 1, 2, 2, 2, 2};
@@ -1142,28 +1210,45 @@ static int num_cus() {
   return cache[dev];
 }
 
-template <int BM, int BN, int WGM, int WGN, int SPS, int STAGES, int EPI, typename TOut>
+template <int BM, int BN, int WGM, int WGN, int SPS, int STAGES, int EPI, typename TOut,
+          bool WAVE_STAGED = false>
 static int launch_pipe(const void* a, const void* w, const void* bias, bool bias_bf16, void* c,
                        int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc, bool vec_store,
                        hipStream_t s) {
-  static_assert(STAGES * (BM + BN) * 64 * SPS + (WGM * WGN) * kScrFloats * 4 <= 160 * 1024,
-                "LDS budget of one CU");
+  constexpr int kStages = STAGES * (BM + BN) * 64 * SPS;
+  static_assert(kStages + (WGM * WGN) * kScrFloats * 4 <= 160 * 1024, "LDS budget of one CU");
+  constexpr int kWaveRowB = BN / WGN * static_cast<int>(sizeof(TOut));
+  static_assert(!WAVE_STAGED || (kStages + 16 * kWaveRowB * WGM * WGN <= 160 * 1024 &&
+                                 kWaveRowB % 128 == 0),
+                "wave-staged output: LDS budget and whole lines per wave row");
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = (N + BN - 1) / BN;
   const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
   if (tiles > 0x7fffffff) return CGPT_ESHAPE;
   const int grid = static_cast<int>(tiles < num_cus() ? tiles : num_cus());
   // Buffer-resource stores write whole 4-column groups and address one tile's
-  // rows with 31-bit byte offsets.
+  // rows with 31-bit byte offsets; staged stores write whole 16-byte chunks.
   const bool buf_store = vec_store && N % 4 == 0 &&
                          static_cast<int64_t>(BM) * ldc * static_cast<int64_t>(sizeof(TOut)) < 0x7fffffff;
+  constexpr int EPC = 16 / static_cast<int>(sizeof(TOut));
+  const bool staged = WAVE_STAGED && buf_store && N % EPC == 0 && ldc % EPC == 0 &&
+                      reinterpret_cast<uintptr_t>(c) % 16 == 0;
+  if constexpr (WAVE_STAGED) {
+    if (staged) {
+      hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut, kOutWaveStaged>),
+                         dim3(grid), dim3(64 * WGM * WGN), 0, s, static_cast<const bf16_t*>(a),
+                         static_cast<const bf16_t*>(w), bias, bias_bf16, static_cast<TOut*>(c), M,
+                         N, K, lda, ldw, ldc, tiles_m, tiles_n, vec_store);
+      return hip_status(hipGetLastError());
+    }
+  }
   if (buf_store)
-    hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut, true>), dim3(grid),
+    hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut, kOutBuffer>), dim3(grid),
                        dim3(64 * WGM * WGN), 0, s, static_cast<const bf16_t*>(a),
                        static_cast<const bf16_t*>(w), bias, bias_bf16, static_cast<TOut*>(c), M, N,
                        K, lda, ldw, ldc, tiles_m, tiles_n, vec_store);
   else
-    hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut, false>), dim3(grid),
+    hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut, kOutPlain>), dim3(grid),
                        dim3(64 * WGM * WGN), 0, s, static_cast<const bf16_t*>(a),
                        static_cast<const bf16_t*>(w), bias, bias_bf16, static_cast<TOut*>(c), M, N,
                        K, lda, ldw, ldc, tiles_m, tiles_n, vec_store);
@@ -1274,8 +1359,8 @@ static int launch_tile(int tile, const void* a, const void* w, const void* bias,
         return launch_slab<256, 192, 2, 4, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda, ldw,
                                                       ldc, vec_store, s);
       case 15:
-        return launch_slab<256, 256, 2, 4, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda, ldw,
-                                                      ldc, vec_store, s);
+        return launch_pipe<256, 256, 2, 4, 2, 2, EPI, TOut, true>(a, w, bias, bias_bf16, c, M, N, K,
+                                                                  lda, ldw, ldc, vec_store, s);
       default: return CGPT_EINVAL;
     }
   } else {

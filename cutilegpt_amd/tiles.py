@@ -22,6 +22,9 @@ Tile ids index the configuration table compiled into libcgpt.so
     previous slab's MFMAs run, output rows staged through LDS and stored as
     whole lines (rows of 16-byte multiples; otherwise the 2-stage kernel):
           14 = 256x192 (8 waves of 128x48)
+    bf16, the 2-stage 256x256 pipeline with each wave's output rows staged
+    through its own LDS slot and stored as whole lines:
+          15 = 256x256 (8 waves of 128x64)
     fp32: 0 = 128x128, 1 = 64x64
 
 ``TABLE`` maps exact (dtype, M, N, K) problems measured on MI355X to the tile
@@ -42,14 +45,14 @@ TABLE: Dict[Tuple[int, int, int, int], int] = {
     # GPT-2 124M prefill, M = 16 x 1024
     (_B, 16384, 2304, 768): 14,   # c_attn       981
     (_B, 16384, 768, 768): 14,    # attn c_proj  841
-    (_B, 16384, 3072, 768): 12,   # c_fc         865 (GELU epilogue: 12 is faster in the model)
+    (_B, 16384, 3072, 768): 15,   # c_fc         992 (867 with the GELU epilogue)
     (_B, 16384, 768, 3072): 14,   # mlp c_proj  1202
-    (_B, 16384, 50304, 768): 12,  # lm head (vocab padded), fp32 out 809
+    (_B, 16384, 50304, 768): 15,  # lm head (vocab padded), fp32 out 830
     # 'medium' (8L, d 512) prefill, M = 16 x 256
     (_B, 4096, 1536, 512): 14,    # 431
     (_B, 4096, 2048, 512): 14,    # 533
     (_B, 4096, 512, 2048): 3,     # 271
-    (_B, 4096, 50304, 512): 5,    # lm head (vocab padded), fp32 out 666
+    (_B, 4096, 50304, 512): 15,   # lm head (vocab padded), fp32 out 699
 }
 
 

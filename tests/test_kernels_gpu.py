@@ -131,7 +131,7 @@ def test_gemm_every_bf16_tile(gpu, tile, m, n, k):
     close(out, gemm_ref(a, w, b, _lib.EPI_BIAS), 1e-3, 2 ** -8, f"tile {tile}")
 
 
-DMA_TILES = [5, 6, 7, 8, 9, 10, 11, 12, 13, 14]
+DMA_TILES = [5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15]
 
 
 @pytest.mark.parametrize("tile", DMA_TILES)
@@ -148,7 +148,7 @@ def test_gemm_dma_tiles(gpu, tile, m, n, k, epi):
     close(out, ref, 1e-4 * math.sqrt(k / 64), 1e-5, f"dma tile {tile} {m}x{n}x{k}")
 
 
-PERSIST_TILES = [5, 7, 9, 10, 11, 12, 13, 14]
+PERSIST_TILES = [5, 7, 9, 10, 11, 12, 13, 14, 15]
 
 
 @pytest.mark.parametrize("tile", PERSIST_TILES)
