@@ -131,8 +131,8 @@ class DecodeSession:
                                      c_ptr, B, n, k, k, w.stride(0), n, ac, ac, out_code, epi,
                                      pws, nws, pcnt, ncnt, s), "gemm_skinny")
 
-        def add_ln(delta_ptr, wk):
-            chk(lib.cgpt_add_layernorm(px, delta_ptr, px if delta_ptr else None,
+        def add_ln(delta_ptr, wk, keep_x=True):
+            chk(lib.cgpt_add_layernorm(px, delta_ptr, px if delta_ptr and keep_x else None,
                                        W[wk + ".weight"].data_ptr(), W[wk + ".bias"].data_ptr(),
                                        ph, B, D, 1e-5, f32, ac, ac, ac, s), "add_layernorm")
 
@@ -159,7 +159,8 @@ class DecodeSession:
                  _lib.EPI_BIAS_GELU, ac)
             gemm(pf, W[p + "mlp.c_proj.weight"], W[p + "mlp.c_proj.bias"], pd, D, 4 * D,
                  _lib.EPI_BIAS, ac)
-            add_ln(pd, f"h.{i + 1}.ln_1" if i + 1 < cfg.n_layer else "ln_f")
+            last = i + 1 == cfg.n_layer
+            add_ln(pd, "ln_f" if last else f"h.{i + 1}.ln_1", keep_x=not last)
         gemm(ph, W["lm_head.weight"], None, self.logits.data_ptr(), V, D, _lib.EPI_NONE,
              _DT[self.logits.dtype])
 

@@ -210,9 +210,10 @@ class CutileGPT:
                               M, n, k, k, w.stride(0), n, ac, ac, out_code, epi, t, s), tag)
             mark(tag, False)
 
-        def add_ln(delta_ptr, wk):
+        def add_ln(delta_ptr, wk, keep_x=True):
+            # keep_x=False: the residual sum is not needed again (final LN).
             mark("ln", True)
-            chk(lib.cgpt_add_layernorm(px, delta_ptr, px if delta_ptr else None,
+            chk(lib.cgpt_add_layernorm(px, delta_ptr, px if delta_ptr and keep_x else None,
                                        W[wk + ".weight"].data_ptr(), W[wk + ".bias"].data_ptr(),
                                        ph, M, D, 1e-5, f32, ac, ac, ac, s), "add_layernorm")
             mark("ln", False)
@@ -248,7 +249,8 @@ class CutileGPT:
                  4 * D, D, _lib.EPI_BIAS_GELU, ac)
             gemm("gemm_mlp_proj", pf, W[p + "mlp.c_proj.weight"], W[p + "mlp.c_proj.bias"], pd,
                  D, 4 * D, _lib.EPI_BIAS, ac)
-            add_ln(pd, f"h.{i + 1}.ln_1" if i + 1 < cfg.n_layer else "ln_f")
+            last = i + 1 == cfg.n_layer
+            add_ln(pd, "ln_f" if last else f"h.{i + 1}.ln_1", keep_x=not last)
         if logits_out is not None:
             # Last position of each sequence: rows b*T + T-1 of h, stride T*D.
             mark("lm_head", True)

@@ -167,6 +167,33 @@ def test_gemm_persistent_tiles(gpu, tile, m, n, k, epi):
     close(out, ref, 2e-3, 2 ** -8, f"persistent tile {tile} {m}x{n}x{k}")
 
 
+@pytest.mark.parametrize("tile", [14, 15])
+@pytest.mark.parametrize("ldc_pad,c_off,out_dtype", [(0, 0, BF16), (8, 0, BF16), (4, 4, BF16),
+                                                      (0, 0, F32), (4, 0, F32), (0, 2, F32)])
+def test_gemm_staged_output_layouts(gpu, tile, ldc_pad, c_off, out_dtype):
+    """Staged whole-line stores (tiles 14, 15) with padded output rows and a C pointer that
+    is only 8/4-byte aligned: the aligned cases take the staged path, the others fall back
+    to per-group buffer stores; every element outside the N columns keeps its old value."""
+    m, n, k = 300, 520, 192
+    a = randn(m, k, seed=31, dtype=BF16).to(gpu)
+    w = randn(n, k, seed=32, dtype=BF16, scale=0.05).to(gpu)
+    b = randn(n, seed=33, dtype=BF16).to(gpu)
+    ldc = n + ldc_pad
+    buf = torch.full((m * ldc + c_off + 8,), 7.0, device=gpu, dtype=out_dtype)
+    c = buf[c_off:]
+    lib = _lib.load()
+    odt = _lib.CGPT_BF16 if out_dtype == BF16 else _lib.CGPT_F32
+    _lib.check(lib.cgpt_gemm(a.data_ptr(), w.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, k, k,
+                             ldc, _lib.CGPT_BF16, _lib.CGPT_BF16, odt, _lib.EPI_BIAS_GELU, tile,
+                             torch.cuda.current_stream().cuda_stream), "staged")
+    out = c[:m * ldc].view(m, ldc)
+    ref = gemm_ref(a.cpu(), w.cpu(), b.cpu(), _lib.EPI_BIAS_GELU)
+    tol = (2e-3, 2 ** -8) if out_dtype == BF16 else (1e-4, 1e-5)
+    close(out[:, :n], ref, *tol, f"staged tile {tile} ldc {ldc} off {c_off}")
+    assert torch.all(out[:, n:] == 7.0)
+    assert torch.all(buf[:c_off] == 7.0) and torch.all(buf[c_off + m * ldc:] == 7.0)
+
+
 def test_gemm_pipe_rejects_ragged_k(gpu):
     a = randn(64, 72, dtype=BF16).to(gpu)
     w = randn(64, 72, dtype=BF16).to(gpu)
