@@ -66,6 +66,19 @@ __device__ __forceinline__ void load_vec(const bf16_t* p, float* out) {
     out[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
   }
 }
+// The same conversions for 16 bytes already in registers.
+template <typename T> __device__ __forceinline__ void unpack_vec(const u32x4_t& v, float* out);
+template <> __device__ __forceinline__ void unpack_vec<float>(const u32x4_t& v, float* out) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) out[i] = __uint_as_float(v[i]);
+}
+template <> __device__ __forceinline__ void unpack_vec<bf16_t>(const u32x4_t& v, float* out) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(v[i] << 16);
+    out[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
+  }
+}
 __device__ __forceinline__ void store_vec(float* p, const float* in) {
   f32x4_t v = {in[0], in[1], in[2], in[3]};
   *reinterpret_cast<f32x4_t*>(p) = v;

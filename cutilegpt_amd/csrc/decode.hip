@@ -1,14 +1,7 @@
 // Incremental (KV-cache) decoding kernels: the pieces a greedy generation
-// step needs beyond the prefill kernels.
+// step needs beyond the prefill kernels (the decode-shaped GEMM is in
+// skinny.hip).
 //
-//  * gemm_skinny_kernel — C[M,N] = epi(A W^T + bias) for M <= 64 (one row per
-//    sequence in the batch).  Decode GEMMs are weight-streaming: every weight
-//    byte is read once per step, so the kernel is built around HBM traffic,
-//    not MFMA reuse: W rows go straight from global memory into MFMA fragments
-//    (no LDS staging), several full cache lines per lane in flight, against
-//    the (L2-resident) activation rows; K is split across the waves of a block
-//    and, with a caller workspace, across blocks (deterministic fix-up by the
-//    last block of each column slice).
 //  * attn_decode_kernel — one block per (batch, head): appends the step's key
 //    and value to the cache at position pos, then softmax(q K^T * scale) V
 //    over cache rows 0..pos.  pos = pos_base + *pos_dev, read on the device so
@@ -22,288 +15,6 @@
 #include <limits.h>
 
 namespace cgpt {
-
-// --------------------------------------------------------------- skinny GEMM
-
-constexpr int kSkWaves = 8;      // waves per block, splitting the block's K range
-constexpr int kSkNT = 4;         // 16-column n-tiles per block (64 columns)
-constexpr int kSkU = 2;          // double slabs in flight per wave
-constexpr int kSkTargetBlocks = 512;
-constexpr int kSkMaxSplit = 16;  // K chunks per column slice at most
-constexpr int kCpolSc1 = 16;     // buffer cache-policy bits: sc1 (agent scope)
-
-__device__ __forceinline__ float bias_value(const void* bias, bool bf16, int n) {
-  return bf16 ? bf16_to_f32(static_cast<const bf16_t*>(bias)[n]) : static_cast<const float*>(bias)[n];
-}
-
-// Work split shared by the launcher and the workspace query: 64-column slices
-// x `split` K chunks.
-struct SkinnyPlan {
-  int slices, dslabs, split, mt;
-  int64_t ws_floats;  // per-block partial tiles, all blocks
-};
-
-static SkinnyPlan skinny_plan(int M, int N, int K, int elem_bytes, bool have_ws) {
-  SkinnyPlan p;
-  const int kd = 8 * (16 / elem_bytes);  // k per double slab
-  p.mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
-  p.slices = (N + 16 * kSkNT - 1) / (16 * kSkNT);
-  p.dslabs = (K + kd - 1) / kd;
-  int split = 1;
-  if (have_ws) {
-    // About kSkTargetBlocks blocks, but every wave of a block keeps at least
-    // one double slab and at most kSkMaxSplit chunks per slice.
-    split = (kSkTargetBlocks + p.slices - 1) / p.slices;
-    int cap = p.dslabs / kSkWaves;
-    cap = cap < kSkMaxSplit ? cap : kSkMaxSplit;
-    split = split < cap ? split : cap;
-    split = split > 1 ? split : 1;
-  }
-  p.split = split;
-  p.ws_floats = split > 1 ? static_cast<int64_t>(p.slices) * split * p.mt * kSkNT * 64 * 4 : 0;
-  return p;
-}
-
-// C[M,N] = epi(A W^T + bias) for M <= 16 * MT.  Block = 64 output columns
-// (4 n-tiles) x one K chunk; its 8 waves split the chunk and stream W rows
-// straight into MFMA fragments.  A "double slab" covers 2 * 4 * EPC k: lane
-// group g loads 32 contiguous bytes of each row (k = 2g EPC .. 2g EPC + 2 EPC),
-// so the 4 groups of a row read one full 128-byte line per load pair; the two
-// 16-byte halves feed two MFMAs (any consistent assignment of k to MFMA slots
-// gives the same sums, and A uses the same one).  Partial tiles are summed
-// across waves through LDS in wave order; with split > 1 each block writes its
-// sum to the workspace and the last block of a slice (counted on a device
-// atomic) adds the split partials in chunk order, applies the epilogue and
-// resets the counter — deterministic, and no clearing is needed between calls.
-template <typename TIn, int MT, int EPI, typename TOut>
-__global__ __launch_bounds__(64 * kSkWaves) void gemm_skinny_kernel(
-    const TIn* __restrict__ A, const TIn* __restrict__ W, const void* __restrict__ bias,
-    bool bias_bf16, TOut* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldw,
-    int64_t ldc, bool vec_store, int split, int dslabs, float* __restrict__ ws,
-    int* __restrict__ counters) {
-  constexpr int EPC = 16 / sizeof(TIn);  // elements per 16-byte half
-  constexpr int KD = 8 * EPC;            // k per double slab
-  constexpr int U = kSkU;
-  constexpr int NT = kSkNT;
-  __shared__ f32x4_t red[kSkWaves][MT][NT][64];
-  __shared__ int s_last;
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nb = blockIdx.x / split, sk = blockIdx.x % split;
-  const int n0 = nb * 16 * NT;
-  const int r16 = lane & 15, g = lane >> 4;
-  const int kl = g * 2 * EPC;  // this lane's first k inside a double slab
-  // Rows past N / M are clamped (loaded, never stored).
-  const TIn* wrow[NT];
-#pragma unroll
-  for (int j = 0; j < NT; ++j) wrow[j] = W + static_cast<int64_t>(min(n0 + 16 * j + r16, N - 1)) * ldw;
-  const TIn* arow[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) arow[mt] = A + static_cast<int64_t>(min(16 * mt + r16, M - 1)) * lda;
-
-  const int per_blk = (dslabs + split - 1) / split;
-  const int d0 = sk * per_blk, d1 = min(dslabs, d0 + per_blk);
-  const int cnt = d1 > d0 ? d1 - d0 : 0;
-  const int per_w = (cnt + kSkWaves - 1) / kSkWaves;
-  const int w0 = d0 + wave * per_w, w1 = min(d1, w0 + per_w);
-
-  f32x4_t acc[MT][NT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int j = 0; j < NT; ++j) acc[mt][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  for (int d = w0; d < w1; d += U) {
-    u32x4_t wf[U][NT][2], af[U][MT][2];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        // Halves past K or past this wave's range load the row's first
-        // chunk and are zeroed (K is a multiple of EPC).
-        const int k = (d + u) * KD + kl + h * EPC;
-        const bool ok = (d + u < w1) && (k < K);
-        const int off = ok ? k : 0;
-#pragma unroll
-        for (int j = 0; j < NT; ++j) wf[u][j][h] = *reinterpret_cast<const u32x4_t*>(wrow[j] + off);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) af[u][mt][h] = *reinterpret_cast<const u32x4_t*>(arow[mt] + off);
-        if (!ok) {
-#pragma unroll
-          for (int j = 0; j < NT; ++j) wf[u][j][h] = u32x4_t{0u, 0u, 0u, 0u};
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) af[u][mt][h] = u32x4_t{0u, 0u, 0u, 0u};
-        }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int j = 0; j < NT; ++j) Mfma<TIn>::run(wf[u][j][h], af[u][mt][h], acc[mt][j]);
-  }
-
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int j = 0; j < NT; ++j) red[wave][mt][j][lane] = acc[mt][j];
-  __syncthreads();
-
-  // One (m-tile, n-tile) pair per wave and pass: its sum over the waves.
-  constexpr int kPairs = MT * NT;
-  constexpr int kTile = kPairs * 64;  // f32x4 per block tile
-  f32x4_t sum[(kPairs + kSkWaves - 1) / kSkWaves];
-#pragma unroll
-  for (int q = 0; q < (kPairs + kSkWaves - 1) / kSkWaves; ++q) {
-    const int pr = wave + q * kSkWaves;
-    if (pr < kPairs) {
-      const int mt = pr / NT, j = pr % NT;
-      f32x4_t t = red[0][mt][j][lane];
-#pragma unroll
-      for (int w = 1; w < kSkWaves; ++w) t += red[w][mt][j][lane];
-      sum[q] = t;
-    }
-  }
-
-  if (split > 1) {
-    // Cross-block hand-off without cache-wide fences (an agent-scope fence
-    // writes back and invalidates this XCD's whole L2): partials are stored
-    // and loaded with agent-scope cache policy (sc1), which makes those
-    // accesses coherent across the XCDs' L2s, the same encoding the memory
-    // model uses for agent-scope atomic loads and stores.  The s_waitcnt
-    // before the barrier completes every thread's partial stores before
-    // thread 0 counts the block with a device atomic.
-    const __amdgpu_buffer_rsrc_t rws = __builtin_amdgcn_make_buffer_rsrc(
-        ws + static_cast<int64_t>(nb) * split * kTile * 4, 0, split * kTile * 16, 0x00020000);
-#pragma unroll
-    for (int q = 0; q < (kPairs + kSkWaves - 1) / kSkWaves; ++q) {
-      const int pr = wave + q * kSkWaves;
-      if (pr < kPairs)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, sum[q]), rws,
-                                               (sk * kTile + pr * 64 + lane) * 16, 0, kCpolSc1);
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0)
-      s_last = __hip_atomic_fetch_add(&counters[nb], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-               split - 1;
-    __syncthreads();
-    if (!s_last) return;
-#pragma unroll
-    for (int q = 0; q < (kPairs + kSkWaves - 1) / kSkWaves; ++q) {
-      const int pr = wave + q * kSkWaves;
-      if (pr < kPairs) {
-        // All partials in flight at once, then summed in chunk order.
-        u32x4_t part[kSkMaxSplit];
-#pragma unroll
-        for (int c = 0; c < kSkMaxSplit; ++c)
-          if (c < split)
-            part[c] = __builtin_amdgcn_raw_buffer_load_b128(rws, (c * kTile + pr * 64 + lane) * 16, 0,
-                                                            kCpolSc1);
-        f32x4_t t = __builtin_bit_cast(f32x4_t, part[0]);
-#pragma unroll
-        for (int c = 1; c < kSkMaxSplit; ++c)
-          if (c < split) t += __builtin_bit_cast(f32x4_t, part[c]);
-        sum[q] = t;
-      }
-    }
-    if (threadIdx.x == 0)
-      __hip_atomic_store(&counters[nb], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-
-#pragma unroll
-  for (int q = 0; q < (kPairs + kSkWaves - 1) / kSkWaves; ++q) {
-    const int pr = wave + q * kSkWaves;
-    if (pr >= kPairs) continue;
-    const int mt = pr / NT, j = pr % NT;
-    const int m = 16 * mt + r16, n = n0 + 16 * j + 4 * g;
-    float v[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float x = sum[q][r];
-      if (EPI != CGPT_EPI_NONE) x += n + r < N ? bias_value(bias, bias_bf16, n + r) : 0.f;
-      if (EPI == CGPT_EPI_BIAS_GELU) x = gelu_tanh(x);
-      v[r] = x;
-    }
-    if (m < M && n < N) {
-      TOut* out = C + static_cast<int64_t>(m) * ldc + n;
-      if (vec_store && n + 3 < N) {
-        store4_out(out, v);
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (n + r < N) Elem<TOut>::store(out + r, v[r]);
-      }
-    }
-  }
-}
-
-template <typename TIn, int EPI, typename TOut>
-static int launch_skinny_mt(const SkinnyPlan& p, const void* a, const void* w, const void* bias,
-                            bool bias_bf16, void* c, int M, int N, int K, int64_t lda, int64_t ldw,
-                            int64_t ldc, bool vec_store, float* ws, int* counters, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>(p.slices * p.split)), block(64 * kSkWaves);
-  const TIn* A = static_cast<const TIn*>(a);
-  const TIn* W = static_cast<const TIn*>(w);
-  TOut* C = static_cast<TOut*>(c);
-  if (p.mt == 1)
-    hipLaunchKernelGGL((gemm_skinny_kernel<TIn, 1, EPI, TOut>), grid, block, 0, s, A, W, bias,
-                       bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store, p.split, p.dslabs, ws, counters);
-  else if (p.mt == 2)
-    hipLaunchKernelGGL((gemm_skinny_kernel<TIn, 2, EPI, TOut>), grid, block, 0, s, A, W, bias,
-                       bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store, p.split, p.dslabs, ws, counters);
-  else
-    hipLaunchKernelGGL((gemm_skinny_kernel<TIn, 4, EPI, TOut>), grid, block, 0, s, A, W, bias,
-                       bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store, p.split, p.dslabs, ws, counters);
-  return hip_status(hipGetLastError());
-}
-
-template <typename TIn, typename TOut>
-static int launch_skinny_epi(const SkinnyPlan& p, int epi, const void* a, const void* w,
-                             const void* bias, bool bias_bf16, void* c, int M, int N, int K,
-                             int64_t lda, int64_t ldw, int64_t ldc, bool vec_store, float* ws,
-                             int* counters, hipStream_t s) {
-  switch (epi) {
-    case CGPT_EPI_NONE:
-      return launch_skinny_mt<TIn, CGPT_EPI_NONE, TOut>(p, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s);
-    case CGPT_EPI_BIAS:
-      return launch_skinny_mt<TIn, CGPT_EPI_BIAS, TOut>(p, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s);
-    case CGPT_EPI_BIAS_GELU:
-      return launch_skinny_mt<TIn, CGPT_EPI_BIAS_GELU, TOut>(p, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s);
-    default:
-      return CGPT_EINVAL;
-  }
-}
-
-int launch_gemm_skinny(bool bf16_in, int epilogue, const void* a, const void* w, const void* bias,
-                       bool bias_bf16, void* c, bool out_bf16, int M, int N, int K, int64_t lda,
-                       int64_t ldw, int64_t ldc, void* workspace, int64_t ws_bytes, int* counters,
-                       int64_t n_counters, hipStream_t s) {
-  if (M > 64) return CGPT_ESHAPE;
-  SkinnyPlan p = skinny_plan(M, N, K, bf16_in ? 2 : 4, workspace != nullptr && counters != nullptr);
-  if (p.split > 1 && (p.ws_floats * 4 > ws_bytes || p.slices > n_counters ||
-                      (reinterpret_cast<uintptr_t>(workspace) & 15)))
-    return CGPT_EINVAL;
-  const uintptr_t oa = out_bf16 ? 7 : 15;
-  const bool vec_store = ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(c) & oa) == 0;
-  float* ws = static_cast<float*>(workspace);
-  if (bf16_in)
-    return out_bf16 ? launch_skinny_epi<bf16_t, bf16_t>(p, epilogue, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s)
-                    : launch_skinny_epi<bf16_t, float>(p, epilogue, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s);
-  return out_bf16 ? launch_skinny_epi<float, bf16_t>(p, epilogue, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s)
-                  : launch_skinny_epi<float, float>(p, epilogue, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s);
-}
-
-int skinny_workspace(int M, int N, int K, bool bf16_in, int64_t* ws_bytes, int64_t* n_counters) {
-  const SkinnyPlan p = skinny_plan(M, N, K, bf16_in ? 2 : 4, true);
-  *ws_bytes = p.ws_floats * 4;
-  *n_counters = p.split > 1 ? p.slices : 0;
-  return CGPT_OK;
-}
 
 // ------------------------------------------------------- decode attention
 
@@ -335,20 +46,47 @@ template <typename T> __device__ __forceinline__ float round_to(float x);
 template <> __device__ __forceinline__ float round_to<float>(float x) { return x; }
 template <> __device__ __forceinline__ float round_to<bf16_t>(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
+// The step's q, k and v for one decode-attention call: T rows (direct), or
+// the fused QKV GEMM's split-K partial products plus its bias — columns
+// q_off / k_off / v_off + h * hd of row b, P[s] at parts + s * part_stride —
+// added in chunk order and rounded to T as the GEMM's own output would be.
 template <typename T>
+struct DecIn {
+  const T* q;
+  const T* kn;
+  const T* vn;
+  int64_t q_sb, q_sh, kn_sb, kn_sh, vn_sb, vn_sh;
+  const float* parts;
+  int n_parts;
+  int64_t part_stride, ldp, q_off, k_off, v_off;
+  const T* bias;
+};
+
+// One block per (batch, head), keys in chunks of kDecThreads.  Thread
+// (kg, cv) = (tid / NV, tid % NV) owns 16-byte column vector cv of keys
+// kg, kg + KG, ... of a chunk for both K and V, so a wave's loads cover whole
+// cache rows; a chunk's K and V loads are all issued before the first is
+// used, through buffer resources whose record count ends at row pos (rows at
+// and past pos read as zero: the new row comes from registers, and nothing is
+// read back from the cache rows this block writes).  Scores are dot products
+// reduced across the NV lanes of a key; softmax runs online across chunks
+// (one chunk for pos < kDecThreads).  P is rounded to T before the P V
+// product, as in the prefill kernel.
+template <typename T, int NV, int MAXP>
 __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(
-    const T* __restrict__ q, const T* __restrict__ kn, const T* __restrict__ vn, T* __restrict__ kc,
-    T* __restrict__ vc, T* __restrict__ o, int H, int hd, int Tmax, int pos_base,
-    const int* __restrict__ pos_dev, int64_t q_sb, int64_t q_sh, int64_t kn_sb, int64_t kn_sh,
-    int64_t vn_sb, int64_t vn_sh, int64_t c_sb, int64_t c_sh, int64_t c_st, int64_t o_sb,
-    int64_t o_sh, float scale_log2, int* err_flag) {
+    DecIn<T> in, T* __restrict__ kc, T* __restrict__ vc, T* __restrict__ o, int H, int Tmax,
+    int pos_base, const int* __restrict__ pos_dev, int64_t c_sb, int64_t c_sh, int64_t c_st,
+    int64_t o_sb, int64_t o_sh, float scale_log2, int* err_flag) {
   constexpr int EPV = Elem<T>::kVec;  // elements per 16-byte vector
-  extern __shared__ float dsm[];
-  float* qs = dsm;                     // hd
-  float* sc = qs + hd;                 // Tmax scores, then probabilities
-  float* part = sc + Tmax;             // kDecThreads * 8 partial outputs
-  float* scr = part + kDecThreads * 8; // kDecWaves
+  constexpr int HD = NV * EPV;
+  constexpr int KG = kDecThreads / NV;  // keys per chunk a column lane visits: NV
+  constexpr int R3 = (3 * HD + kDecThreads - 1) / kDecThreads;
+  __shared__ float qs[HD], kns[HD], vns[HD];
+  __shared__ float sc[kDecThreads];
+  __shared__ float part[KG][HD];
+  __shared__ float scr[kDecWaves];
   const int tid = threadIdx.x;
+  const int kg = tid / NV, cv = tid % NV;
   const int b = blockIdx.x / H, h = blockIdx.x % H;
   int pos = pos_base + (pos_dev != nullptr ? *pos_dev : 0);
   if (pos < 0 || pos >= Tmax) {
@@ -358,64 +96,142 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(
   const int Tk = pos + 1;
   T* kcb = kc + b * c_sb + h * c_sh;
   T* vcb = vc + b * c_sb + h * c_sh;
-  const T* knb = kn + b * kn_sb + h * kn_sh;
-  const T* vnb = vn + b * vn_sb + h * vn_sh;
-  const T* qb = q + b * q_sb + h * q_sh;
-  for (int d = tid; d < hd; d += kDecThreads) {
-    kcb[pos * c_st + d] = knb[d];
-    vcb[pos * c_st + d] = vnb[d];
-    qs[d] = Elem<T>::load(qb + d);
-  }
-  __syncthreads();  // the appended row and q are visible to the whole block
+  const int row_bytes = static_cast<int>(c_st * sizeof(T));
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(kcb, 0, pos * row_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(vcb, 0, pos * row_bytes, 0x00020000);
 
-  float mx = -INFINITY;
-  for (int j = tid; j < Tk; j += kDecThreads) {
-    const T* kr = kcb + j * c_st;
-    float s = 0.f;
-    for (int d = 0; d < hd; d += EPV) {
-      float kv[EPV];
-      load_vec(kr + d, kv);
+  // The step's q / k / v values: thread tid + r * kDecThreads holds value i of
+  // the 3 * HD (q | k | v).
+  float sv[R3];
+  if (MAXP == 0) {
 #pragma unroll
-      for (int e = 0; e < EPV; ++e) s = fmaf(qs[d + e], kv[e], s);
+    for (int r = 0; r < R3; ++r) {
+      const int i = tid + r * kDecThreads, which = i / HD, d = i % HD;
+      const T* src = which == 0 ? in.q + b * in.q_sb + h * in.q_sh
+                   : which == 1 ? in.kn + b * in.kn_sb + h * in.kn_sh
+                                : in.vn + b * in.vn_sb + h * in.vn_sh;
+      sv[r] = i < 3 * HD ? Elem<T>::load(src + d) : 0.f;
     }
-    s *= scale_log2;
-    sc[j] = s;
-    mx = fmaxf(mx, s);
+  } else {
+    // Partials past n_parts lie past the record count and read as zero.
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(in.parts), 0, static_cast<int>(in.n_parts * in.part_stride * 4), 0x00020000);
+    float pv[R3][MAXP];
+#pragma unroll
+    for (int r = 0; r < R3; ++r) {
+      const int i = tid + r * kDecThreads, which = i / HD, d = i % HD;
+      const int64_t col = (which == 0 ? in.q_off : which == 1 ? in.k_off : in.v_off) + h * HD + d;
+      const uint32_t off = static_cast<uint32_t>((b * in.ldp + col) * 4);
+#pragma unroll
+      for (int s = 0; s < MAXP; ++s)
+        pv[r][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+            rp, s < in.n_parts && i < 3 * HD ? off + static_cast<uint32_t>(s * in.part_stride * 4) : 0x80000000u,
+            0, 0));
+    }
+#pragma unroll
+    for (int r = 0; r < R3; ++r) {
+      const int i = tid + r * kDecThreads, which = i / HD, d = i % HD;
+      const int64_t col = (which == 0 ? in.q_off : which == 1 ? in.k_off : in.v_off) + h * HD + d;
+      float t = pv[r][0];
+#pragma unroll
+      for (int s = 1; s < MAXP; ++s)
+        if (s < in.n_parts) t += pv[r][s];
+      sv[r] = i < 3 * HD ? round_to<T>(t + Elem<T>::load(in.bias + col)) : 0.f;
+    }
   }
-  mx = block_reduce<true>(mx, scr);
-  float sum = 0.f;
-  for (int j = tid; j < Tk; j += kDecThreads) {
-    const float p = __builtin_amdgcn_exp2f(sc[j] - mx);
-    sc[j] = p;
-    sum += p;
-  }
-  sum = block_reduce<false>(sum, scr);  // its barriers also publish sc
 
-  // P V: key group kg = tid / TPR handles keys kg, kg + KG, ...; its TPR
-  // threads each own EPV consecutive dims of the row (one 16-byte load per
-  // key).  P is rounded to the storage type before the product, as in the
-  // prefill kernel.  The KG group sums are then added through LDS.
-  const int tpr = hd / EPV;            // threads per value row
-  const int kgroups = kDecThreads / tpr;
-  const int kg = tid / tpr, c0 = (tid % tpr) * EPV;
+  float mrun = -INFINITY, lsum = 0.f;
   float acc[EPV];
 #pragma unroll
   for (int e = 0; e < EPV; ++e) acc[e] = 0.f;
-  for (int j = kg; j < Tk; j += kgroups) {
-    float vv[EPV];
-    load_vec(vcb + j * c_st + c0, vv);
-    const float p = round_to<T>(sc[j]);
+
+  for (int c0 = 0; c0 < Tk; c0 += kDecThreads) {
+    // This chunk's K and V vectors, all in flight together.
+    u32x4_t kr[NV], vr[NV];
 #pragma unroll
-    for (int e = 0; e < EPV; ++e) acc[e] = fmaf(p, vv[e], acc[e]);
+    for (int i = 0; i < NV; ++i) {
+      const uint32_t off = static_cast<uint32_t>((c0 + kg + KG * i) * row_bytes + cv * 16);
+      kr[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0);
+      vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
+    }
+    if (c0 == 0) {
+      // Publish q / k / v and append k, v at row pos of the cache.
+#pragma unroll
+      for (int r = 0; r < R3; ++r) {
+        const int i = tid + r * kDecThreads, which = i / HD, d = i % HD;
+        if (i < 3 * HD) {
+          if (which == 0) {
+            qs[d] = sv[r];
+          } else if (which == 1) {
+            kns[d] = sv[r];
+            Elem<T>::store(kcb + pos * c_st + d, sv[r]);
+          } else {
+            vns[d] = sv[r];
+            Elem<T>::store(vcb + pos * c_st + d, sv[r]);
+          }
+        }
+      }
+      __syncthreads();
+    }
+    float qv[EPV];
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) qv[e] = qs[cv * EPV + e];
+    // Partial dot products of this lane's column vector, then summed over the
+    // NV lanes of each key (consecutive lanes).
+    float s[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      float kv[EPV];
+      unpack_vec<T>(kr[i], kv);
+      if (c0 + kg + KG * i == pos) {
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) kv[e] = kns[cv * EPV + e];
+      }
+      float t = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) t = fmaf(qv[e], kv[e], t);
+      s[i] = t;
+    }
+#pragma unroll
+    for (int off = 1; off < NV; off <<= 1)
+#pragma unroll
+      for (int i = 0; i < NV; ++i) s[i] += __shfl_xor(s[i], off, 64);
+    if (cv == 0) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) sc[kg + KG * i] = s[i] * scale_log2;
+    }
+    __syncthreads();
+    const float sj = c0 + tid < Tk ? sc[tid] : -INFINITY;
+    const float mnew = fmaxf(mrun, block_reduce<true>(sj, scr));
+    const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
+    const float p = c0 + tid < Tk ? __builtin_amdgcn_exp2f(sj - mnew) : 0.f;
+    lsum = lsum * alpha + block_reduce<false>(p, scr);
+    mrun = mnew;
+    sc[tid] = round_to<T>(p);  // sc[tid] was read by this thread only since the barrier
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) acc[e] *= alpha;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      float vv[EPV];
+      unpack_vec<T>(vr[i], vv);
+      if (c0 + kg + KG * i == pos) {
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) vv[e] = vns[cv * EPV + e];
+      }
+      const float pj = sc[kg + KG * i];
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) acc[e] = fmaf(pj, vv[e], acc[e]);
+    }
+    __syncthreads();  // sc is rewritten by the next chunk
   }
-  // part holds kDecThreads * EPV floats: [group][dim]
 #pragma unroll
-  for (int e = 0; e < EPV; ++e) part[kg * hd + c0 + e] = acc[e];
+  for (int e = 0; e < EPV; ++e) part[kg][cv * EPV + e] = acc[e];
   __syncthreads();
-  if (tid < hd) {
+  for (int d = tid; d < HD; d += kDecThreads) {
     float t = 0.f;
-    for (int k = 0; k < kgroups; ++k) t += part[k * hd + tid];
-    Elem<T>::store(o + b * o_sb + h * o_sh + tid, t / sum);
+    for (int k = 0; k < KG; ++k) t += part[k][d];
+    Elem<T>::store(o + b * o_sb + h * o_sh + d, t / lsum);
   }
 }
 
@@ -500,6 +316,75 @@ __global__ __launch_bounds__(kAmThreads) void argmax_kernel(const T* __restrict_
   }
 }
 
+template <typename T, int MAXP>
+static void launch_dec_nv(int nv, const DecIn<T>& in, T* kc, T* vc, T* o, int64_t BH, int H, int tm,
+                          int pb, const int* pos_dev, int64_t c_sb, int64_t c_sh, int64_t c_st,
+                          int64_t o_sb, int64_t o_sh, float sl2, int* err, hipStream_t s) {
+#define CGPT_DEC_NV(N)                                                                              \
+  case N:                                                                                           \
+    hipLaunchKernelGGL((attn_decode_kernel<T, N, MAXP>), dim3(static_cast<unsigned>(BH)),           \
+                       dim3(kDecThreads), 0, s, in, kc, vc, o, H, tm, pb, pos_dev, c_sb, c_sh, c_st, \
+                       o_sb, o_sh, sl2, err);                                                       \
+    break;
+  switch (nv) {
+    CGPT_DEC_NV(1)
+    CGPT_DEC_NV(2)
+    CGPT_DEC_NV(4)
+    CGPT_DEC_NV(8)
+    CGPT_DEC_NV(16)
+    CGPT_DEC_NV(32)
+    default:
+      break;
+  }
+#undef CGPT_DEC_NV
+}
+
+// Checks shared by both decode-attention entry points; the q / k / v sources
+// are checked by each.
+static int check_decode(int64_t B, int64_t H, int64_t head_dim, int64_t t_max, int64_t pos_base,
+                        const int* pos_dev, const void* k_cache, const void* v_cache, const void* o,
+                        int64_t c_sb, int64_t c_sh, int64_t c_st, int dtype) {
+  if (B < 0 || H <= 0 || head_dim <= 0 || t_max <= 0) return CGPT_EINVAL;
+  if (!k_cache || !v_cache || !o) return CGPT_EINVAL;
+  if (dtype != CGPT_F32 && dtype != CGPT_BF16) return CGPT_EDTYPE;
+  const int64_t es = dtype == CGPT_F32 ? 4 : 2, epv = 16 / es;
+  // head_dim = NV 16-byte vectors, NV a power of two dividing kDecThreads, at most 32.
+  const int64_t nv = head_dim / epv;
+  if (head_dim % epv != 0 || nv > 32 || (nv & (nv - 1)) != 0) return CGPT_ESHAPE;
+  if (B * H > 0x7fffffff || t_max > 0x7fffffff) return CGPT_ESHAPE;
+  // Cache rows are read as 16-byte vectors through 32-bit buffer offsets.
+  if (c_st % epv != 0 || c_sh % epv != 0 || c_sb % epv != 0 || c_st < head_dim) return CGPT_EINVAL;
+  if (t_max * c_st * es >= (int64_t{1} << 31)) return CGPT_ESHAPE;
+  if ((reinterpret_cast<uintptr_t>(k_cache) & 15) || (reinterpret_cast<uintptr_t>(v_cache) & 15))
+    return CGPT_EINVAL;
+  if (pos_dev == nullptr && (pos_base < 0 || pos_base >= t_max)) return CGPT_EINVAL;
+  return CGPT_OK;
+}
+
+template <typename T>
+static int launch_decode(const DecIn<T>& in, int maxp, void* k_cache, void* v_cache, void* o,
+                         int64_t B, int64_t H, int64_t head_dim, int64_t t_max, int64_t pos_base,
+                         const int* pos_dev, int64_t c_sb, int64_t c_sh, int64_t c_st, int64_t o_sb,
+                         int64_t o_sh, float scale, int* err_flag, void* stream) {
+  const int nv = static_cast<int>(head_dim / Elem<T>::kVec);
+  T* kc = static_cast<T*>(k_cache);
+  T* vc = static_cast<T*>(v_cache);
+  T* op = static_cast<T*>(o);
+  const float sl2 = scale * 1.4426950408889634f;
+  const int hh = static_cast<int>(H), tm = static_cast<int>(t_max), pb = static_cast<int>(pos_base);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t bh = B * H;
+  if (maxp == 0)
+    launch_dec_nv<T, 0>(nv, in, kc, vc, op, bh, hh, tm, pb, pos_dev, c_sb, c_sh, c_st, o_sb, o_sh, sl2, err_flag, s);
+  else if (maxp <= 4)
+    launch_dec_nv<T, 4>(nv, in, kc, vc, op, bh, hh, tm, pb, pos_dev, c_sb, c_sh, c_st, o_sb, o_sh, sl2, err_flag, s);
+  else if (maxp <= 8)
+    launch_dec_nv<T, 8>(nv, in, kc, vc, op, bh, hh, tm, pb, pos_dev, c_sb, c_sh, c_st, o_sb, o_sh, sl2, err_flag, s);
+  else
+    launch_dec_nv<T, 16>(nv, in, kc, vc, op, bh, hh, tm, pb, pos_dev, c_sb, c_sh, c_st, o_sb, o_sh, sl2, err_flag, s);
+  return hip_status(hipGetLastError());
+}
+
 }  // namespace cgpt
 
 using namespace cgpt;
@@ -512,36 +397,51 @@ extern "C" int cgpt_attention_decode(const void* q, const void* k_new, const voi
                                      int64_t c_sb, int64_t c_sh, int64_t c_st, int64_t o_sb,
                                      int64_t o_sh, float scale, int dtype, int* err_flag,
                                      void* stream) {
-  if (B < 0 || H <= 0 || head_dim <= 0 || t_max <= 0) return CGPT_EINVAL;
-  if (B == 0) return CGPT_OK;
-  if (!q || !k_new || !v_new || !k_cache || !v_cache || !o) return CGPT_EINVAL;
-  if (dtype != CGPT_F32 && dtype != CGPT_BF16) return CGPT_EDTYPE;
-  const int epv = dtype == CGPT_F32 ? 4 : 8;
-  if (head_dim > kDecThreads || kDecThreads % head_dim != 0 || head_dim % epv != 0) return CGPT_ESHAPE;
-  if (t_max > 8192 || B * H > 0x7fffffff) return CGPT_ESHAPE;  // dynamic LDS <= 64 KiB
-  // Cache rows are read as 16-byte vectors.
-  if (c_st % epv != 0 || c_sh % epv != 0 || c_sb % epv != 0 || c_st < head_dim) return CGPT_EINVAL;
-  if ((reinterpret_cast<uintptr_t>(k_cache) & 15) || (reinterpret_cast<uintptr_t>(v_cache) & 15))
-    return CGPT_EINVAL;
-  if (pos_dev == nullptr && (pos_base < 0 || pos_base >= t_max)) return CGPT_EINVAL;
-  const size_t smem = (static_cast<size_t>(head_dim) + t_max + kDecThreads * 8 + kDecWaves) * sizeof(float);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const float sl2 = scale * 1.4426950408889634f;
-  const int hh = static_cast<int>(H), hd = static_cast<int>(head_dim), tm = static_cast<int>(t_max);
-  const int pb = static_cast<int>(pos_base);
-  if (dtype == CGPT_BF16)
-    hipLaunchKernelGGL(attn_decode_kernel<bf16_t>, dim3(static_cast<unsigned>(B * H)), dim3(kDecThreads),
-                       smem, s, static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k_new),
-                       static_cast<const bf16_t*>(v_new), static_cast<bf16_t*>(k_cache),
-                       static_cast<bf16_t*>(v_cache), static_cast<bf16_t*>(o), hh, hd, tm, pb, pos_dev,
-                       q_sb, q_sh, kn_sb, kn_sh, vn_sb, vn_sh, c_sb, c_sh, c_st, o_sb, o_sh, sl2, err_flag);
-  else
-    hipLaunchKernelGGL(attn_decode_kernel<float>, dim3(static_cast<unsigned>(B * H)), dim3(kDecThreads),
-                       smem, s, static_cast<const float*>(q), static_cast<const float*>(k_new),
-                       static_cast<const float*>(v_new), static_cast<float*>(k_cache),
-                       static_cast<float*>(v_cache), static_cast<float*>(o), hh, hd, tm, pb, pos_dev,
-                       q_sb, q_sh, kn_sb, kn_sh, vn_sb, vn_sh, c_sb, c_sh, c_st, o_sb, o_sh, sl2, err_flag);
-  return hip_status(hipGetLastError());
+  const int st = check_decode(B, H, head_dim, t_max, pos_base, pos_dev, k_cache, v_cache, o, c_sb,
+                              c_sh, c_st, dtype);
+  if (st != CGPT_OK || B == 0) return st;
+  if (!q || !k_new || !v_new) return CGPT_EINVAL;
+  if (dtype == CGPT_BF16) {
+    DecIn<bf16_t> in{static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k_new),
+                     static_cast<const bf16_t*>(v_new), q_sb, q_sh, kn_sb, kn_sh, vn_sb, vn_sh,
+                     nullptr, 0, 0, 0, 0, 0, 0, nullptr};
+    return launch_decode(in, 0, k_cache, v_cache, o, B, H, head_dim, t_max, pos_base, pos_dev, c_sb,
+                         c_sh, c_st, o_sb, o_sh, scale, err_flag, stream);
+  }
+  DecIn<float> in{static_cast<const float*>(q), static_cast<const float*>(k_new),
+                  static_cast<const float*>(v_new), q_sb, q_sh, kn_sb, kn_sh, vn_sb, vn_sh,
+                  nullptr, 0, 0, 0, 0, 0, 0, nullptr};
+  return launch_decode(in, 0, k_cache, v_cache, o, B, H, head_dim, t_max, pos_base, pos_dev, c_sb,
+                       c_sh, c_st, o_sb, o_sh, scale, err_flag, stream);
+}
+
+extern "C" int cgpt_attention_decode_partials(
+    const float* qkv_partials, int64_t n_parts, int64_t part_stride, int64_t ldp,
+    const void* qkv_bias, int64_t q_off, int64_t k_off, int64_t v_off, void* k_cache,
+    void* v_cache, void* o, int64_t B, int64_t H, int64_t head_dim, int64_t t_max,
+    int64_t pos_base, const int* pos_dev, int64_t c_sb, int64_t c_sh, int64_t c_st, int64_t o_sb,
+    int64_t o_sh, float scale, int dtype, int* err_flag, void* stream) {
+  const int st = check_decode(B, H, head_dim, t_max, pos_base, pos_dev, k_cache, v_cache, o, c_sb,
+                              c_sh, c_st, dtype);
+  if (st != CGPT_OK || B == 0) return st;
+  if (!qkv_partials || !qkv_bias) return CGPT_EINVAL;
+  if (n_parts < 1 || n_parts > 16 || q_off < 0 || k_off < 0 || v_off < 0) return CGPT_EINVAL;
+  const int64_t width = H * head_dim;  // columns of q, of k and of v
+  const int64_t hi = (q_off > k_off ? q_off : k_off) > v_off ? (q_off > k_off ? q_off : k_off) : v_off;
+  if (ldp < hi + width || part_stride < (B - 1) * ldp + hi + width) return CGPT_EINVAL;
+  if (n_parts * part_stride * 4 >= (int64_t{1} << 31)) return CGPT_ESHAPE;
+  if (dtype == CGPT_BF16) {
+    DecIn<bf16_t> in{nullptr, nullptr, nullptr, 0, 0, 0, 0, 0, 0, qkv_partials,
+                     static_cast<int>(n_parts), part_stride, ldp, q_off, k_off, v_off,
+                     static_cast<const bf16_t*>(qkv_bias)};
+    return launch_decode(in, static_cast<int>(n_parts), k_cache, v_cache, o, B, H, head_dim, t_max,
+                         pos_base, pos_dev, c_sb, c_sh, c_st, o_sb, o_sh, scale, err_flag, stream);
+  }
+  DecIn<float> in{nullptr, nullptr, nullptr, 0, 0, 0, 0, 0, 0, qkv_partials,
+                  static_cast<int>(n_parts), part_stride, ldp, q_off, k_off, v_off,
+                  static_cast<const float*>(qkv_bias)};
+  return launch_decode(in, static_cast<int>(n_parts), k_cache, v_cache, o, B, H, head_dim, t_max,
+                       pos_base, pos_dev, c_sb, c_sh, c_st, o_sb, o_sh, scale, err_flag, stream);
 }
 
 extern "C" int cgpt_kv_store(const void* k, const void* v, void* k_cache, void* v_cache, int64_t B,

@@ -1464,6 +1464,32 @@ extern "C" int cgpt_gemm_skinny(const void* a, const void* w, const void* bias, 
                             n_counters, static_cast<hipStream_t>(stream));
 }
 
+extern "C" int cgpt_gemm_partials_plan(int64_t M, int64_t N, int64_t K, int in_dtype,
+                                       int64_t* n_split) {
+  using namespace cgpt;
+  if (!n_split || M <= 0 || M > 64 || N <= 0 || K <= 0) return CGPT_EINVAL;
+  if (N > 0x7fffffff || K > 0x7fffffff) return CGPT_ESHAPE;
+  if (in_dtype != CGPT_F32 && in_dtype != CGPT_BF16) return CGPT_EDTYPE;
+  *n_split = gemm_partials_split(static_cast<int>(M), static_cast<int>(N), static_cast<int>(K),
+                                 in_dtype == CGPT_BF16);
+  return CGPT_OK;
+}
+
+extern "C" int cgpt_gemm_partials(const void* a, const void* w, float* partials, int64_t M,
+                                  int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldp,
+                                  int64_t n_split, int in_dtype, void* stream) {
+  using namespace cgpt;
+  const int st = validate_gemm(a, w, nullptr, partials, M, N, K, lda, ldw, ldp, in_dtype, in_dtype,
+                               CGPT_F32, CGPT_EPI_NONE);
+  if (st != CGPT_OK || M == 0 || N == 0) return st;
+  if (M > 64) return CGPT_ESHAPE;
+  if (reinterpret_cast<uintptr_t>(partials) & 3) return CGPT_EINVAL;
+  if (n_split < 1 || n_split > 0x7fffffff) return CGPT_EINVAL;
+  return launch_gemm_partials(in_dtype == CGPT_BF16, a, w, partials, static_cast<int>(M),
+                              static_cast<int>(N), static_cast<int>(K), lda, ldw, ldp,
+                              static_cast<int>(n_split), static_cast<hipStream_t>(stream));
+}
+
 extern "C" int cgpt_gemm(const void* a, const void* w, const void* bias, void* c, int64_t M,
                          int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldc, int in_dtype,
                          int bias_dtype, int out_dtype, int epilogue, int tile, void* stream) {

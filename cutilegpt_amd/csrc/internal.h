@@ -6,7 +6,7 @@
 
 namespace cgpt {
 
-// Skinny GEMM (M <= 64): C[M,N] = epilogue(A W^T + bias).  64-column slices of
+// Skinny GEMM (M <= 64): C[M,N] = epilogue(A W^T + bias).  Column slices of
 // C, K split across the block's waves and (when workspace and counters are
 // given) across blocks.  Arguments as cgpt_gemm's, already validated
 // (K % (16 / element size) == 0, 16-byte aligned A and W rows).
@@ -17,5 +17,12 @@ int launch_gemm_skinny(bool bf16_in, int epilogue, const void* a, const void* w,
 
 // Workspace bytes and counters the split-K skinny GEMM uses for (M, N, K).
 int skinny_workspace(int M, int N, int K, bool bf16_in, int64_t* ws_bytes, int64_t* n_counters);
+
+// Split-K partial products P[s][m][n] (fp32, P[s] at partials + s * M * ldp)
+// of the skinny GEMM, for a consumer that adds them; the split the kernel is
+// tuned for, and the launch.
+int gemm_partials_split(int M, int N, int K, bool bf16_in);
+int launch_gemm_partials(bool bf16_in, const void* a, const void* w, float* partials, int M, int N,
+                         int K, int64_t lda, int64_t ldw, int64_t ldp, int split, hipStream_t s);
 
 }  // namespace cgpt

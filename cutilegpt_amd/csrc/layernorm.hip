@@ -167,6 +167,143 @@ static int launch_ln1(int delta_dtype, int y_dtype, const void* x, const void* d
   return CGPT_EDTYPE;
 }
 
+// ---- residual + LayerNorm over split-K partial products (decode steps)
+//
+// delta[r][c] = round_to(TD, P[0][r][c] + ... + P[n-1][r][c] + bias[c]) (the
+// value the GEMM would have stored), then as add_layernorm_kernel.  A row is
+// short (a decode step has one row per sequence) and its partials are n times
+// its size, so a 256-thread block takes one row: thread t owns columns
+// [4(256c + t), +4) for chunk c, and every load of the row (x, the n partials,
+// bias, gamma, beta) is issued before any is used.  Partials past n read as
+// zero from past their buffer's record count.
+constexpr int kLnpThreads = 256;
+
+template <typename TD> __device__ __forceinline__ float round_delta(float v);
+template <> __device__ __forceinline__ float round_delta<float>(float v) { return v; }
+template <> __device__ __forceinline__ float round_delta<bf16_t>(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+template <typename TD, typename TY, int MAXCH, int MAXP>
+__global__ __launch_bounds__(kLnpThreads) void add_layernorm_partials_kernel(
+    const float* __restrict__ x, const float* __restrict__ parts, int n_parts, int part_stride,
+    int ldp, const void* __restrict__ bias, float* x_out, const void* __restrict__ gamma,
+    const void* __restrict__ beta, bool param_bf16, TY* __restrict__ y, int cols, float eps) {
+  __shared__ float scr[kLnpThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int row = blockIdx.x;
+  const int64_t base = static_cast<int64_t>(row) * cols;
+  const int pshift = param_bf16 ? 1 : 2;
+  const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(gamma), 0, cols << pshift, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(beta), 0, cols << pshift, 0x00020000);
+  // No bias: a zero record count makes every bias load read zero.
+  const __amdgpu_buffer_rsrc_t rbi = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(bias), 0, bias != nullptr ? cols << pshift : 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(parts), 0, n_parts * part_stride * 4, 0x00020000);
+  float v[MAXCH][4], gm[MAXCH][4], bt[MAXCH][4], bi[MAXCH][4];
+  u32x4_t praw[MAXCH][MAXP], graw[MAXCH], braw[MAXCH], biraw[MAXCH];
+#pragma unroll
+  for (int c = 0; c < MAXCH; ++c) {
+    const int col = (c * kLnpThreads + tid) * 4;
+    const int cc = col < cols ? col : 0;
+    load4(x + base + cc, v[c]);
+#pragma unroll
+    for (int s = 0; s < MAXP; ++s)
+      praw[c][s] = __builtin_amdgcn_raw_buffer_load_b128(
+          rp, s < n_parts ? static_cast<uint32_t>(((s * part_stride) + row * ldp + cc) * 4) : 0x80000000u,
+          0, 0);
+    graw[c] = __builtin_amdgcn_raw_buffer_load_b128(rg, cc << pshift, 0, 0);
+    braw[c] = __builtin_amdgcn_raw_buffer_load_b128(rb, cc << pshift, 0, 0);
+    biraw[c] = __builtin_amdgcn_raw_buffer_load_b128(rbi, cc << pshift, 0, 0);
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int c = 0; c < MAXCH; ++c) {
+    const bool ok = (c * kLnpThreads + tid) * 4 < cols;
+    decode_param(graw[c], param_bf16, gm[c]);
+    decode_param(braw[c], param_bf16, bt[c]);
+    decode_param(biraw[c], param_bf16, bi[c]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float d = __uint_as_float(praw[c][0][j]);
+#pragma unroll
+      for (int s = 1; s < MAXP; ++s)
+        if (s < n_parts) d += __uint_as_float(praw[c][s][j]);
+      const float t = v[c][j] + round_delta<TD>(d + bi[c][j]);
+      v[c][j] = ok ? t : 0.f;
+      sum += v[c][j];
+    }
+  }
+  // Block sums in wave order; correctly rounded divisions as the row kernel.
+  const float n_f = static_cast<float>(cols);
+  float ws = wave_sum(sum);
+  if (lane == 0) scr[wave] = ws;
+  __syncthreads();
+  float tot = scr[0];
+#pragma unroll
+  for (int w = 1; w < kLnpThreads / 64; ++w) tot += scr[w];
+  const float mean = tot / n_f;
+  float sq = 0.f;
+#pragma unroll
+  for (int c = 0; c < MAXCH; ++c) {
+    const bool ok = (c * kLnpThreads + tid) * 4 < cols;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float t = v[c][j] - mean;
+      sq += ok ? t * t : 0.f;
+    }
+  }
+  ws = wave_sum(sq);
+  __syncthreads();  // every wave has read scr
+  if (lane == 0) scr[wave] = ws;
+  __syncthreads();
+  tot = scr[0];
+#pragma unroll
+  for (int w = 1; w < kLnpThreads / 64; ++w) tot += scr[w];
+  const float rstd = 1.0f / sqrtf(tot / n_f + eps);
+#pragma unroll
+  for (int c = 0; c < MAXCH; ++c) {
+    const int col = (c * kLnpThreads + tid) * 4;
+    if (col < cols) {
+      if (x_out != nullptr) store4(x_out + base + col, v[c]);
+      float o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = (v[c][j] - mean) * rstd * gm[c][j] + bt[c][j];
+      store4(y + base + col, o);
+    }
+  }
+}
+
+template <typename TD, typename TY, int MAXCH>
+static void launch_lnp_p(int maxp, const float* x, const float* parts, int n, int ps, int ldp,
+                         const void* bias, float* x_out, const void* gamma, const void* beta,
+                         bool pb, TY* y, int rows, int cols, float eps, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(rows)), block(kLnpThreads);
+  if (maxp <= 2)
+    hipLaunchKernelGGL((add_layernorm_partials_kernel<TD, TY, MAXCH, 2>), grid, block, 0, s, x, parts, n, ps, ldp, bias, x_out, gamma, beta, pb, y, cols, eps);
+  else if (maxp <= 4)
+    hipLaunchKernelGGL((add_layernorm_partials_kernel<TD, TY, MAXCH, 4>), grid, block, 0, s, x, parts, n, ps, ldp, bias, x_out, gamma, beta, pb, y, cols, eps);
+  else if (maxp <= 8)
+    hipLaunchKernelGGL((add_layernorm_partials_kernel<TD, TY, MAXCH, 8>), grid, block, 0, s, x, parts, n, ps, ldp, bias, x_out, gamma, beta, pb, y, cols, eps);
+  else
+    hipLaunchKernelGGL((add_layernorm_partials_kernel<TD, TY, MAXCH, 16>), grid, block, 0, s, x, parts, n, ps, ldp, bias, x_out, gamma, beta, pb, y, cols, eps);
+}
+
+template <typename TD, typename TY>
+static int launch_lnp(const float* x, const float* parts, int n, int ps, int ldp, const void* bias,
+                      float* x_out, const void* gamma, const void* beta, bool pb, void* y,
+                      int rows, int cols, float eps, hipStream_t s) {
+  TY* yp = static_cast<TY*>(y);
+  if (cols <= 1024)
+    launch_lnp_p<TD, TY, 1>(n, x, parts, n, ps, ldp, bias, x_out, gamma, beta, pb, yp, rows, cols, eps, s);
+  else if (cols <= 2048)
+    launch_lnp_p<TD, TY, 2>(n, x, parts, n, ps, ldp, bias, x_out, gamma, beta, pb, yp, rows, cols, eps, s);
+  else
+    launch_lnp_p<TD, TY, 4>(n, x, parts, n, ps, ldp, bias, x_out, gamma, beta, pb, yp, rows, cols, eps, s);
+  return hip_status(hipGetLastError());
+}
+
 static bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7) == 0; }
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 static bool dtype_ok(int d) { return d == CGPT_F32 || d == CGPT_BF16; }
@@ -200,4 +337,42 @@ extern "C" int cgpt_add_layernorm(const void* x, const void* delta, void* x_out,
   if (x_dtype == CGPT_F32)
     return launch_ln1<float>(delta_dtype, y_dtype, x, delta, x_out, gamma, beta, pb, y, rows, c, eps, s);
   return launch_ln1<bf16_t>(delta_dtype, y_dtype, x, delta, x_out, gamma, beta, pb, y, rows, c, eps, s);
+}
+
+extern "C" int cgpt_add_layernorm_partials(const void* x, const float* partials, int64_t n_parts,
+                                           int64_t part_stride, int64_t ldp, const void* bias,
+                                           void* x_out, const void* gamma, const void* beta,
+                                           void* y, int64_t rows, int64_t cols, float eps,
+                                           int x_dtype, int delta_dtype, int param_dtype,
+                                           int y_dtype, void* stream) {
+  using namespace cgpt;
+  if (rows < 0 || cols <= 0) return CGPT_EINVAL;
+  if (rows == 0) return CGPT_OK;
+  if (x == nullptr || partials == nullptr || gamma == nullptr || beta == nullptr || y == nullptr)
+    return CGPT_EINVAL;
+  if (x_dtype != CGPT_F32 || !dtype_ok(delta_dtype) || !dtype_ok(param_dtype) || !dtype_ok(y_dtype))
+    return CGPT_EDTYPE;
+  if (cols % 4 != 0 || cols > 4096 || rows > 0x7fffffff) return CGPT_ESHAPE;
+  if (n_parts < 1 || n_parts > 16 || ldp < cols || ldp % 4 != 0 || part_stride % 4 != 0 ||
+      part_stride < (rows - 1) * ldp + cols)
+    return CGPT_EINVAL;
+  if (n_parts * part_stride * 4 >= (int64_t{1} << 31)) return CGPT_ESHAPE;
+  if (!aligned16(partials) || !ptr_aligned(x, x_dtype) || !ptr_aligned(x_out, x_dtype) ||
+      !ptr_aligned(y, y_dtype) || !ptr_aligned(gamma, param_dtype) ||
+      !ptr_aligned(beta, param_dtype) || !ptr_aligned(bias, param_dtype))
+    return CGPT_EINVAL;
+  if (!(eps >= 0.f)) return CGPT_EINVAL;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool pb = param_dtype == CGPT_BF16;
+  const int r = static_cast<int>(rows), c = static_cast<int>(cols), n = static_cast<int>(n_parts);
+  const int ps = static_cast<int>(part_stride), lp = static_cast<int>(ldp);
+  const float* xp = static_cast<const float*>(x);
+  float* xo = static_cast<float*>(x_out);
+  if (delta_dtype == CGPT_BF16)
+    return y_dtype == CGPT_BF16
+               ? launch_lnp<bf16_t, bf16_t>(xp, partials, n, ps, lp, bias, xo, gamma, beta, pb, y, r, c, eps, s)
+               : launch_lnp<bf16_t, float>(xp, partials, n, ps, lp, bias, xo, gamma, beta, pb, y, r, c, eps, s);
+  return y_dtype == CGPT_BF16
+             ? launch_lnp<float, bf16_t>(xp, partials, n, ps, lp, bias, xo, gamma, beta, pb, y, r, c, eps, s)
+             : launch_lnp<float, float>(xp, partials, n, ps, lp, bias, xo, gamma, beta, pb, y, r, c, eps, s);
 }

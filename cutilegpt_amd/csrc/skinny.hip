@@ -1,0 +1,455 @@
+// Weight-streaming GEMM for decode shapes: C[M,N] = epi(A W^T + bias) with
+// M <= 64 (one row per sequence of a decode batch).  Every weight byte is read
+// once per call, so the kernel is built around memory round trips, not MFMA
+// reuse:
+//
+//  * a block owns 16*NT output columns (NT n-tiles of W rows) and one K chunk;
+//    its NW waves split the chunk's double slabs evenly;
+//  * a wave issues every W and A fragment load of a round (DPW double slabs)
+//    before its first MFMA, as buffer loads whose out-of-range offsets return
+//    zero (k past K and slots past the wave's range need no select), so a
+//    block costs one memory round trip;
+//  * W rows go straight from global memory into MFMA fragments: lane group g
+//    of a row loads 32 contiguous bytes (k = 2g EPC .. 2g EPC + 2 EPC), the 4
+//    groups of a row one full 128-byte line per load pair; the two 16-byte
+//    halves feed two MFMAs (any consistent assignment of k to MFMA slots gives
+//    the same sums, and A uses the same one);
+//  * partial tiles are summed across the block's waves through LDS in wave
+//    order.  Across K chunks (split > 1) either
+//      - the block's sum goes to a workspace and the last block of a column
+//        slice (counted on a device atomic) adds the chunks in order and
+//        applies the epilogue (cgpt_gemm_skinny), or
+//      - the chunk sums are written as fp32 partial products for the consumer
+//        to add (cgpt_gemm_partials; the decode step's attention and
+//        residual+LayerNorm kernels do), which leaves the GEMM a single
+//        round trip with no cross-block hand-off.
+#include "common.h"
+#include "internal.h"
+
+namespace cgpt {
+
+// Block shapes: NT n-tiles per block, NW waves, DPW double slabs per wave and
+// load round.
+struct SkShape {
+  int nt, nw, dpw;
+};
+constexpr SkShape kSkShapes[] = {{2, 8, 1}, {4, 8, 2}, {2, 16, 2}};
+constexpr int kSkTargetBlocks = 512;  // fix-up path: blocks to aim for
+constexpr int kSkMaxSplit = 16;       // fix-up path: K chunks per column slice at most
+constexpr int kCpolSc1 = 16;          // buffer cache-policy bits: sc1 (agent scope)
+constexpr uint32_t kOob = 0x80000000u;  // past every record count: the load returns 0
+
+__device__ __forceinline__ float bias_value(const void* bias, bool bf16, int n) {
+  return bf16 ? bf16_to_f32(static_cast<const bf16_t*>(bias)[n]) : static_cast<const float*>(bias)[n];
+}
+
+enum SkMode { kSkFinal = 0, kSkPartials = 1 };
+
+template <typename TIn, int MT, int NT, int NW, int DPW, int MODE, int EPI, typename TOut>
+__global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(
+    const TIn* __restrict__ A, const TIn* __restrict__ W, const void* __restrict__ bias,
+    bool bias_bf16, TOut* __restrict__ C, int M, int N, int K, int lda, int ldw, int64_t ldc,
+    bool vec_store, int split, int dslabs, float* __restrict__ ws, int* __restrict__ counters) {
+  constexpr int ES = sizeof(TIn);
+  constexpr int EPC = 16 / ES;  // elements per 16-byte half
+  constexpr int KD = 8 * EPC;   // k per double slab
+  constexpr int P = MT * NT;    // (m-tile, n-tile) pairs of the block tile
+  constexpr int Q = (P + NW - 1) / NW;
+  __shared__ f32x4_t red[NW][P][64];
+  __shared__ int s_last;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nb = blockIdx.x / split, sk = blockIdx.x % split;
+  const int n0 = nb * 16 * NT;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int kl = g * 2 * EPC;  // this lane's first k inside a double slab
+
+  // Record counts end at the last row's K-th element: the host keeps them
+  // below 2^31, so kOob is out of range for both.
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<TIn*>(W), 0, static_cast<int>((N - 1) * ldw * ES + K * ES), 0x00020000);
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<TIn*>(A), 0, static_cast<int>((M - 1) * lda * ES + K * ES), 0x00020000);
+  // Rows past N / M are clamped (loaded, never stored).
+  uint32_t wro[NT], aro[MT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) wro[j] = static_cast<uint32_t>(min(n0 + 16 * j + r16, N - 1)) * ldw * ES;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) aro[mt] = static_cast<uint32_t>(min(16 * mt + r16, M - 1)) * lda * ES;
+
+  const int chunk = (dslabs + split - 1) / split;
+  const int d0 = sk * chunk, d1 = min(dslabs, d0 + chunk);
+  const int cnt = d1 > d0 ? d1 - d0 : 0;
+  const int w0 = d0 + wave * cnt / NW, w1 = d0 + (wave + 1) * cnt / NW;
+
+  f32x4_t acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[mt][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int d = w0; d < w1; d += DPW) {
+    u32x4_t wf[DPW][NT][2], af[DPW][MT][2];
+#pragma unroll
+    for (int u = 0; u < DPW; ++u)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k = (d + u) * KD + kl + h * EPC;
+        const uint32_t kb = (d + u < w1 && k < K) ? static_cast<uint32_t>(k) * ES : kOob;
+#pragma unroll
+        for (int j = 0; j < NT; ++j) wf[u][j][h] = __builtin_amdgcn_raw_buffer_load_b128(rw, wro[j] + kb, 0, 0);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) af[u][mt][h] = __builtin_amdgcn_raw_buffer_load_b128(ra, aro[mt] + kb, 0, 0);
+      }
+    // Keep the round's loads ahead of its MFMAs: interleaving them makes the
+    // compiler wait on each load in turn.
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < DPW; ++u)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int j = 0; j < NT; ++j) Mfma<TIn>::run(wf[u][j][h], af[u][mt][h], acc[mt][j]);
+  }
+
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) red[wave][mt * NT + j][lane] = acc[mt][j];
+  __syncthreads();
+
+  // One (m-tile, n-tile) pair per wave and pass: its sum over the waves.
+  f32x4_t sum[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const int pr = wave + q * NW;
+    if (pr < P) {
+      f32x4_t t = red[0][pr][lane];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) t += red[w][pr][lane];
+      sum[q] = t;
+    }
+  }
+
+  if (MODE == kSkPartials) {
+    // Chunk sk's partial products: ws[sk][m][n], rows of ldc floats.
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const int pr = wave + q * NW;
+      if (pr >= P) continue;
+      const int m = 16 * (pr / NT) + r16, n = n0 + 16 * (pr % NT) + 4 * g;
+      if (m >= M || n >= N) continue;
+      float* out = ws + (static_cast<int64_t>(sk) * M + m) * ldc + n;
+      const float v[4] = {sum[q][0], sum[q][1], sum[q][2], sum[q][3]};
+      if (vec_store && n + 3 < N) {
+        store4_out(out, v);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (n + r < N) out[r] = v[r];
+      }
+    }
+    return;
+  }
+
+  if (split > 1) {
+    // Cross-block hand-off without cache-wide fences (an agent-scope fence
+    // writes back and invalidates this XCD's whole L2): partials are stored
+    // and loaded with agent-scope cache policy (sc1), which makes those
+    // accesses coherent across the XCDs' L2s, the same encoding the memory
+    // model uses for agent-scope atomic loads and stores.  The s_waitcnt
+    // before the barrier completes every thread's partial stores before
+    // thread 0 counts the block with a device atomic.
+    constexpr int kTile = P * 64;  // f32x4 per block tile
+    const __amdgpu_buffer_rsrc_t rws = __builtin_amdgcn_make_buffer_rsrc(
+        ws + static_cast<int64_t>(nb) * split * kTile * 4, 0, split * kTile * 16, 0x00020000);
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const int pr = wave + q * NW;
+      if (pr < P)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, sum[q]), rws,
+                                               (sk * kTile + pr * 64 + lane) * 16, 0, kCpolSc1);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+      s_last = __hip_atomic_fetch_add(&counters[nb], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               split - 1;
+    __syncthreads();
+    if (!s_last) return;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const int pr = wave + q * NW;
+      if (pr < P) {
+        // All partials in flight at once, then summed in chunk order.
+        u32x4_t part[kSkMaxSplit];
+#pragma unroll
+        for (int c = 0; c < kSkMaxSplit; ++c)
+          if (c < split)
+            part[c] = __builtin_amdgcn_raw_buffer_load_b128(rws, (c * kTile + pr * 64 + lane) * 16, 0,
+                                                            kCpolSc1);
+        f32x4_t t = __builtin_bit_cast(f32x4_t, part[0]);
+#pragma unroll
+        for (int c = 1; c < kSkMaxSplit; ++c)
+          if (c < split) t += __builtin_bit_cast(f32x4_t, part[c]);
+        sum[q] = t;
+      }
+    }
+    if (threadIdx.x == 0)
+      __hip_atomic_store(&counters[nb], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const int pr = wave + q * NW;
+    if (pr >= P) continue;
+    const int m = 16 * (pr / NT) + r16, n = n0 + 16 * (pr % NT) + 4 * g;
+    float v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float x = sum[q][r];
+      if (EPI != CGPT_EPI_NONE) x += n + r < N ? bias_value(bias, bias_bf16, n + r) : 0.f;
+      if (EPI == CGPT_EPI_BIAS_GELU) x = gelu_tanh(x);
+      v[r] = x;
+    }
+    if (m < M && n < N) {
+      TOut* out = C + static_cast<int64_t>(m) * ldc + n;
+      if (vec_store && n + 3 < N) {
+        store4_out(out, v);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (n + r < N) Elem<TOut>::store(out + r, v[r]);
+      }
+    }
+  }
+}
+
+// Work split of one call: which block shape, 16*NT-column slices x `split`
+// K chunks.
+struct SkinnyPlan {
+  int shape, mt, slices, dslabs, split;
+  int64_t ws_floats;  // fix-up path: per-block partial tiles, all blocks
+};
+
+static int sk_mt(int M) { return M <= 16 ? 1 : M <= 32 ? 2 : 4; }
+
+// Final output (fix-up split when workspace and counters are given).
+static SkinnyPlan skinny_plan(int M, int N, int K, int elem_bytes, bool have_ws) {
+  SkinnyPlan p;
+  const int kd = 8 * (16 / elem_bytes);
+  p.mt = sk_mt(M);
+  p.dslabs = (K + kd - 1) / kd;
+  const int slices2 = (N + 31) / 32;
+  if (have_ws) {
+    p.shape = 0;
+  } else if (slices2 >= 1024) {
+    p.shape = 1;  // wide N (an LM head): fewer A re-reads per weight byte
+  } else {
+    // 16 waves leave 128 VGPRs a lane: too few for four m-tiles' fragments.
+    p.shape = p.dslabs >= 16 && p.mt < 4 ? 2 : 0;
+  }
+  const SkShape& s = kSkShapes[p.shape];
+  p.slices = (N + 16 * s.nt - 1) / (16 * s.nt);
+  int split = 1;
+  if (have_ws) {
+    // About kSkTargetBlocks blocks, but every wave of a block keeps at least
+    // one double slab and at most kSkMaxSplit chunks per slice.
+    split = (kSkTargetBlocks + p.slices - 1) / p.slices;
+    int cap = p.dslabs / s.nw;
+    cap = cap < kSkMaxSplit ? cap : kSkMaxSplit;
+    split = split < cap ? split : cap;
+    split = split > 1 ? split : 1;
+  }
+  p.split = split;
+  p.ws_floats = split > 1 ? static_cast<int64_t>(p.slices) * split * p.mt * s.nt * 64 * 4 : 0;
+  return p;
+}
+
+// Partial products: chunks of about 5 double slabs (K <= 64 slabs) or 10.
+static SkinnyPlan partials_plan(int M, int N, int K, int elem_bytes, int split) {
+  SkinnyPlan p;
+  const int kd = 8 * (16 / elem_bytes);
+  p.mt = sk_mt(M);
+  p.dslabs = (K + kd - 1) / kd;
+  p.shape = p.dslabs >= 64 ? 1 : 0;
+  const SkShape& s = kSkShapes[p.shape];
+  p.slices = (N + 16 * s.nt - 1) / (16 * s.nt);
+  if (split <= 0) {
+    const int target = p.shape == 1 ? 10 : 5;
+    split = (p.dslabs + target - 1) / target;
+  }
+  p.split = split;
+  p.ws_floats = 0;
+  return p;
+}
+
+template <typename TIn, int MT, int NT, int NW, int DPW, int MODE, int EPI, typename TOut>
+static void launch_one(const SkinnyPlan& p, const TIn* A, const TIn* W, const void* bias,
+                       bool bias_bf16, TOut* C, int M, int N, int K, int lda, int ldw, int64_t ldc,
+                       bool vec_store, float* ws, int* counters, hipStream_t s) {
+  hipLaunchKernelGGL((gemm_skinny_kernel<TIn, MT, NT, NW, DPW, MODE, EPI, TOut>),
+                     dim3(static_cast<unsigned>(p.slices * p.split)), dim3(64 * NW), 0, s, A, W, bias,
+                     bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store, p.split, p.dslabs, ws, counters);
+}
+
+template <typename TIn, int MT, int MODE, int EPI, typename TOut>
+static void launch_shape(const SkinnyPlan& p, const TIn* A, const TIn* W, const void* bias,
+                         bool bias_bf16, TOut* C, int M, int N, int K, int lda, int ldw, int64_t ldc,
+                         bool vec_store, float* ws, int* counters, hipStream_t s) {
+#define CGPT_SK_SHAPE(I)                                                                          \
+  launch_one<TIn, MT, kSkShapes[I].nt, kSkShapes[I].nw, kSkShapes[I].dpw, MODE, EPI, TOut>(        \
+      p, A, W, bias, bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s)
+  if (p.shape == 1) {
+    CGPT_SK_SHAPE(1);
+  } else if constexpr (MT < 4) {  // the planners never give shape 2 four m-tiles
+    if (p.shape == 2)
+      CGPT_SK_SHAPE(2);
+    else
+      CGPT_SK_SHAPE(0);
+  } else {
+    CGPT_SK_SHAPE(0);
+  }
+#undef CGPT_SK_SHAPE
+}
+
+template <typename TIn, int MODE, int EPI, typename TOut>
+static void launch_mt(const SkinnyPlan& p, const TIn* A, const TIn* W, const void* bias,
+                      bool bias_bf16, TOut* C, int M, int N, int K, int lda, int ldw, int64_t ldc,
+                      bool vec_store, float* ws, int* counters, hipStream_t s) {
+  if (p.mt == 1)
+    launch_shape<TIn, 1, MODE, EPI, TOut>(p, A, W, bias, bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s);
+  else if (p.mt == 2)
+    launch_shape<TIn, 2, MODE, EPI, TOut>(p, A, W, bias, bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s);
+  else
+    launch_shape<TIn, 4, MODE, EPI, TOut>(p, A, W, bias, bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s);
+}
+
+template <typename TIn, typename TOut>
+static int launch_final(const SkinnyPlan& p, int epi, const void* a, const void* w, const void* bias,
+                        bool bias_bf16, void* c, int M, int N, int K, int lda, int ldw, int64_t ldc,
+                        bool vec_store, float* ws, int* counters, hipStream_t s) {
+  const TIn* A = static_cast<const TIn*>(a);
+  const TIn* W = static_cast<const TIn*>(w);
+  TOut* C = static_cast<TOut*>(c);
+  switch (epi) {
+    case CGPT_EPI_NONE:
+      launch_mt<TIn, kSkFinal, CGPT_EPI_NONE, TOut>(p, A, W, bias, bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s);
+      break;
+    case CGPT_EPI_BIAS:
+      launch_mt<TIn, kSkFinal, CGPT_EPI_BIAS, TOut>(p, A, W, bias, bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s);
+      break;
+    case CGPT_EPI_BIAS_GELU:
+      launch_mt<TIn, kSkFinal, CGPT_EPI_BIAS_GELU, TOut>(p, A, W, bias, bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s);
+      break;
+    default:
+      return CGPT_EINVAL;
+  }
+  return hip_status(hipGetLastError());
+}
+
+// Buffer offsets are 32-bit: A's rows, and the W rows of one launch, must end
+// below 2^31 bytes.  Returns the columns per launch (a multiple of the slice
+// width), or 0 when even one slice is too large.
+static int cols_per_launch(int N, int K, int64_t ldw, int es, int slice_cols) {
+  const int64_t lim = (int64_t{1} << 31) - static_cast<int64_t>(K) * es;
+  const int64_t rows = lim / (ldw * es) + 1;  // rows r with (r - 1) * ldw * es + K * es < 2^31
+  const int64_t slices = rows / slice_cols;
+  if (slices <= 0) return 0;
+  const int64_t cols = slices * slice_cols;
+  return cols >= N ? N : static_cast<int>(cols);
+}
+
+static bool a_fits(int M, int K, int64_t lda, int es) {
+  return static_cast<int64_t>(M - 1) * lda * es + static_cast<int64_t>(K) * es < (int64_t{1} << 31);
+}
+
+int launch_gemm_skinny(bool bf16_in, int epilogue, const void* a, const void* w, const void* bias,
+                       bool bias_bf16, void* c, bool out_bf16, int M, int N, int K, int64_t lda,
+                       int64_t ldw, int64_t ldc, void* workspace, int64_t ws_bytes, int* counters,
+                       int64_t n_counters, hipStream_t s) {
+  if (M > 64) return CGPT_ESHAPE;
+  const int es = bf16_in ? 2 : 4;
+  const bool have_ws = workspace != nullptr && counters != nullptr;
+  const SkinnyPlan p = skinny_plan(M, N, K, es, have_ws);
+  const int scols = 16 * kSkShapes[p.shape].nt;
+  const int step = cols_per_launch(N, K, ldw, es, scols);
+  if (step == 0 || !a_fits(M, K, lda, es)) return CGPT_ESHAPE;
+  if (p.split > 1 && (p.ws_floats * 4 > ws_bytes || p.slices > n_counters ||
+                      (reinterpret_cast<uintptr_t>(workspace) & 15)))
+    return CGPT_EINVAL;
+  const uintptr_t oa = out_bf16 ? 7 : 15;
+  const bool vec_store = ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(c) & oa) == 0;
+  const int ob = out_bf16 ? 2 : 4, bb = bias_bf16 ? 2 : 4;
+  const int64_t tile_floats = static_cast<int64_t>(p.split) * p.mt * kSkShapes[p.shape].nt * 64 * 4;
+  for (int c0 = 0; c0 < N; c0 += step) {
+    // Column groups start on slice boundaries, so the workspace and counter
+    // slots of a group are its slices' own.
+    const int n = N - c0 < step ? N - c0 : step;
+    SkinnyPlan pg = p;
+    pg.slices = (n + scols - 1) / scols;
+    const int first = c0 / scols;
+    const void* wg = static_cast<const char*>(w) + static_cast<int64_t>(c0) * ldw * es;
+    const void* bg = bias != nullptr ? static_cast<const char*>(bias) + static_cast<int64_t>(c0) * bb : nullptr;
+    void* cg = static_cast<char*>(c) + static_cast<int64_t>(c0) * ob;
+    float* wsg = have_ws ? static_cast<float*>(workspace) + first * tile_floats : nullptr;
+    int* cng = have_ws ? counters + first : nullptr;
+    const int li = static_cast<int>(lda), lw = static_cast<int>(ldw);
+    int st;
+    if (bf16_in)
+      st = out_bf16 ? launch_final<bf16_t, bf16_t>(pg, epilogue, a, wg, bg, bias_bf16, cg, M, n, K, li, lw, ldc, vec_store, wsg, cng, s)
+                    : launch_final<bf16_t, float>(pg, epilogue, a, wg, bg, bias_bf16, cg, M, n, K, li, lw, ldc, vec_store, wsg, cng, s);
+    else
+      st = out_bf16 ? launch_final<float, bf16_t>(pg, epilogue, a, wg, bg, bias_bf16, cg, M, n, K, li, lw, ldc, vec_store, wsg, cng, s)
+                    : launch_final<float, float>(pg, epilogue, a, wg, bg, bias_bf16, cg, M, n, K, li, lw, ldc, vec_store, wsg, cng, s);
+    if (st != CGPT_OK) return st;
+  }
+  return CGPT_OK;
+}
+
+int skinny_workspace(int M, int N, int K, bool bf16_in, int64_t* ws_bytes, int64_t* n_counters) {
+  const SkinnyPlan p = skinny_plan(M, N, K, bf16_in ? 2 : 4, true);
+  *ws_bytes = p.ws_floats * 4;
+  *n_counters = p.split > 1 ? p.slices : 0;
+  return CGPT_OK;
+}
+
+int gemm_partials_split(int M, int N, int K, bool bf16_in) {
+  return partials_plan(M, N, K, bf16_in ? 2 : 4, 0).split;
+}
+
+int launch_gemm_partials(bool bf16_in, const void* a, const void* w, float* partials, int M, int N,
+                         int K, int64_t lda, int64_t ldw, int64_t ldp, int split, hipStream_t s) {
+  if (M > 64) return CGPT_ESHAPE;
+  const int es = bf16_in ? 2 : 4;
+  const SkinnyPlan p = partials_plan(M, N, K, es, split);
+  if (split < 1 || split > p.dslabs) return CGPT_EINVAL;
+  const int scols = 16 * kSkShapes[p.shape].nt;
+  const int step = cols_per_launch(N, K, ldw, es, scols);
+  if (step == 0 || !a_fits(M, K, lda, es)) return CGPT_ESHAPE;
+  const bool vec_store = ldp % 4 == 0 && (reinterpret_cast<uintptr_t>(partials) & 15) == 0;
+  const int li = static_cast<int>(lda), lw = static_cast<int>(ldw);
+  for (int c0 = 0; c0 < N; c0 += step) {
+    const int n = N - c0 < step ? N - c0 : step;
+    SkinnyPlan pg = p;
+    pg.slices = (n + scols - 1) / scols;
+    const void* wg = static_cast<const char*>(w) + static_cast<int64_t>(c0) * ldw * es;
+    float* pp = partials + c0;
+    if (bf16_in)
+      launch_mt<bf16_t, kSkPartials, CGPT_EPI_NONE, float>(
+          pg, static_cast<const bf16_t*>(a), static_cast<const bf16_t*>(wg), nullptr, false, nullptr,
+          M, n, K, li, lw, ldp, vec_store, pp, nullptr, s);
+    else
+      launch_mt<float, kSkPartials, CGPT_EPI_NONE, float>(
+          pg, static_cast<const float*>(a), static_cast<const float*>(wg), nullptr, false, nullptr,
+          M, n, K, li, lw, ldp, vec_store, pp, nullptr, s);
+    const int st = hip_status(hipGetLastError());
+    if (st != CGPT_OK) return st;
+  }
+  return CGPT_OK;
+}
+
+}  // namespace cgpt

@@ -6,11 +6,22 @@ once (prefill) while its keys and values are stored into a per-layer cache,
 and every further token costs one step over B rows:
 
     embedding at position pos        cgpt_embedding_at (pos read on device)
-    per layer: LN, QKV GEMM          cgpt_add_layernorm, cgpt_gemm (skinny, M = B)
-               attention             cgpt_attention_decode (appends k, v at pos)
-               proj, LN, fc+GELU, proj
-    LN_f, LM head                    cgpt_gemm (skinny, N = vocab)
+    LN_1 of layer 0                  cgpt_add_layernorm
+    per layer: QKV GEMM              cgpt_gemm_partials (split-K partial products)
+               attention             cgpt_attention_decode_partials (adds the
+                                     partials + bias, appends k, v at pos)
+               proj GEMM             cgpt_gemm_partials
+               residual + LN_2       cgpt_add_layernorm_partials
+               fc + GELU             cgpt_gemm (skinny, M = B)
+               MLP proj GEMM         cgpt_gemm_partials
+               residual + next LN    cgpt_add_layernorm_partials (LN_f last)
+    LM head                          cgpt_gemm (skinny, N = vocab)
     greedy token                     cgpt_argmax (also written to the history)
+
+The split-K GEMMs leave their K chunks' sums to the kernel that reads their
+output, so a weight-streaming GEMM is one memory round trip with no
+cross-block reduction; ``partials=False`` runs the earlier sequence instead
+(bias GEMMs with an in-kernel split-K fix-up, separate residual+LN).
 
 Everything a step reads or writes lives in buffers allocated once per
 ``generate`` call and the position is a device counter, so the greedy step is
@@ -51,7 +62,7 @@ class KVCache:
 class DecodeSession:
     """Buffers, cache and device counters of one batched generation."""
 
-    def __init__(self, model, B: int, t0: int, max_new: int):
+    def __init__(self, model, B: int, t0: int, max_new: int, partials: bool = True):
         cfg = model.config
         if t0 + max_new > cfg.block_size:
             raise ValueError(f"prompt {t0} + {max_new} new tokens exceeds block_size {cfg.block_size}")
@@ -75,9 +86,22 @@ class DecodeSession:
         self.logits = torch.empty((B, V), dtype=model.logits_dtype, device=dev)
         self.err = torch.zeros(1, dtype=torch.int32, device=dev)
         self.graph: Optional[torch.cuda.CUDAGraph] = None
-        # One split-K workspace + counter array serves every step GEMM (they
-        # run one after another on one stream and leave the counters zero).
         lib = _lib.load()
+        # Split-K partial products of the QKV, attention-projection and
+        # MLP-projection GEMMs, added by the attention and residual+LayerNorm
+        # kernels that consume them (one buffer: the GEMMs run one after
+        # another on one stream).
+        self.partials = partials
+        self.splits = {}
+        p_max = 4
+        for n, k in ((3 * D, D), (D, D), (D, 4 * D)):
+            ns = ctypes.c_int64()
+            _lib.check(lib.cgpt_gemm_partials_plan(B, n, k, _DT[act], ctypes.byref(ns)), "partials plan")
+            self.splits[(n, k)] = ns.value
+            p_max = max(p_max, ns.value * B * n)
+        self.parts = torch.empty(p_max if partials else 4, dtype=torch.float32, device=dev)
+        # One split-K workspace + counter array serves every other step GEMM
+        # (they run one after another on one stream and leave the counters zero).
         ws_max, cnt_max = 0, 0
         for n, k in ((3 * D, D), (D, D), (4 * D, D), (D, 4 * D), (V, D)):
             wb, nc = ctypes.c_int64(), ctypes.c_int64()
@@ -136,6 +160,21 @@ class DecodeSession:
                                        W[wk + ".weight"].data_ptr(), W[wk + ".bias"].data_ptr(),
                                        ph, B, D, 1e-5, f32, ac, ac, ac, s), "add_layernorm")
 
+        pp = self.parts.data_ptr()
+
+        def gemm_parts(a_ptr, w, n, k):
+            ns = self.splits[(n, k)]
+            chk(lib.cgpt_gemm_partials(a_ptr, w.data_ptr(), pp, B, n, k, k, w.stride(0), n, ns,
+                                       ac, s), "gemm_partials")
+            return ns
+
+        def add_ln_parts(ns, bias, wk, keep_x=True):
+            chk(lib.cgpt_add_layernorm_partials(px, pp, ns, B * D, D, bias.data_ptr(),
+                                                px if keep_x else None,
+                                                W[wk + ".weight"].data_ptr(),
+                                                W[wk + ".bias"].data_ptr(), ph, B, D, 1e-5, f32,
+                                                ac, ac, ac, s), "add_layernorm_partials")
+
         chk(lib.cgpt_embedding_at(self.ids.data_ptr(), W["wte"].data_ptr(), W["wpe"].data_ptr(),
                                   px, B, D, V, self.t0, pstep, cfg.block_size, ac, f32,
                                   self.err.data_ptr(), s), "embedding_at")
@@ -145,6 +184,22 @@ class DecodeSession:
         scale = 1.0 / math.sqrt(hd)
         for i in range(cfg.n_layer):
             p = f"h.{i}."
+            last = i + 1 == cfg.n_layer
+            ln_next = "ln_f" if last else f"h.{i + 1}.ln_1"
+            if self.partials:
+                ns = gemm_parts(ph, W[p + "attn.c_attn.weight"], 3 * D, D)
+                chk(lib.cgpt_attention_decode_partials(
+                    pp, ns, B * 3 * D, 3 * D, W[p + "attn.c_attn.bias"].data_ptr(), 0, D, 2 * D,
+                    self.cache.k[i].data_ptr(), self.cache.v[i].data_ptr(), pa, B, H, hd, t_max,
+                    self.t0, pstep, csb, csh, cst, D, hd, scale, ac, self.err.data_ptr(), s),
+                    "attention_decode_partials")
+                ns = gemm_parts(pa, W[p + "attn.c_proj.weight"], D, D)
+                add_ln_parts(ns, W[p + "attn.c_proj.bias"], p + "ln_2")
+                gemm(ph, W[p + "mlp.c_fc.weight"], W[p + "mlp.c_fc.bias"], pf, 4 * D, D,
+                     _lib.EPI_BIAS_GELU, ac)
+                ns = gemm_parts(pf, W[p + "mlp.c_proj.weight"], D, 4 * D)
+                add_ln_parts(ns, W[p + "mlp.c_proj.bias"], ln_next, keep_x=not last)
+                continue
             gemm(ph, W[p + "attn.c_attn.weight"], W[p + "attn.c_attn.bias"], pq, 3 * D, D,
                  _lib.EPI_BIAS, ac)
             chk(lib.cgpt_attention_decode(pq, pq + D * esz, pq + 2 * D * esz,
@@ -159,8 +214,7 @@ class DecodeSession:
                  _lib.EPI_BIAS_GELU, ac)
             gemm(pf, W[p + "mlp.c_proj.weight"], W[p + "mlp.c_proj.bias"], pd, D, 4 * D,
                  _lib.EPI_BIAS, ac)
-            last = i + 1 == cfg.n_layer
-            add_ln(pd, "ln_f" if last else f"h.{i + 1}.ln_1", keep_x=not last)
+            add_ln(pd, ln_next, keep_x=not last)
         gemm(ph, W["lm_head.weight"], None, self.logits.data_ptr(), V, D, _lib.EPI_NONE,
              _DT[self.logits.dtype])
 

@@ -74,6 +74,24 @@ int cgpt_add_layernorm(const void* x, const void* delta, void* x_out,
                        void* stream);
 
 /*
+ * cgpt_add_layernorm with delta given as a GEMM's split-K partial products
+ * (cgpt_gemm_partials): delta[r][c] = P[0][r][c] + ... + P[n_parts-1][r][c]
+ * + bias[c] (bias of param_dtype, may be NULL), added in that order and
+ * rounded to delta_dtype — the value the GEMM's bias epilogue would have
+ * stored — then s = x + delta, x_out, y as cgpt_add_layernorm.  P[s] row r at
+ * partials + s * part_stride + r * ldp (16-byte aligned; ldp and part_stride
+ * multiples of 4); 1 <= n_parts <= 16; x and x_out fp32.  Replaces
+ * cutile_linear_bias + the residual add + cutile_layer_norm at decode shapes
+ * (cutile_gpt/kernels/linear.py:112-222, layernorm.py:77-135,
+ * cutile_gpt/models/gpt.py:155,174).
+ */
+int cgpt_add_layernorm_partials(const void* x, const float* partials, int64_t n_parts,
+                                int64_t part_stride, int64_t ldp, const void* bias, void* x_out,
+                                const void* gamma, const void* beta, void* y, int64_t rows,
+                                int64_t cols, float eps, int x_dtype, int delta_dtype,
+                                int param_dtype, int y_dtype, void* stream);
+
+/*
  * C[M,N] = epilogue(A[M,K] * W[N,K]^T (+ bias[N])).
  * A row-major with leading dimension lda, W row-major (out_features, in_features)
  * with leading dimension ldw — the nn.Linear / cutileGPT `weight` layout, so no
@@ -121,6 +139,27 @@ int cgpt_gemm_skinny(const void* a, const void* w, const void* bias, void* c,
 /* Workspace bytes and counters cgpt_gemm_skinny needs for (M, N, K, in_dtype). */
 int cgpt_gemm_skinny_workspace(int64_t M, int64_t N, int64_t K, int in_dtype,
                                int64_t* workspace_bytes, int64_t* n_counters);
+
+/*
+ * Split-K partial products of a decode-shaped GEMM (M <= 64), left for the
+ * consumer to add: P[s][m][n] = sum over k in chunk s of A[m,k] W[n,k] (fp32,
+ * no bias), s < n_split, P[s] at partials + s * M * ldp (row stride ldp >= N
+ * floats, partials 4-byte aligned).  K is cut into n_split chunks of
+ * ceil(dslabs / n_split) double slabs (a double slab = 64 bf16 or 32 fp32 k);
+ * 1 <= n_split <= dslabs.  Adding P[0] .. P[n_split-1] in order, plus the bias,
+ * gives cgpt_gemm's result up to fp32 summation order; the decode step hands
+ * them to cgpt_attention_decode_partials and cgpt_add_layernorm_partials, so
+ * the GEMM is one memory round trip with no cross-block reduction.
+ * A and W requirements as cgpt_gemm.  Replaces cutile_linear_bias at decode
+ * shapes, cutile_gpt/kernels/linear.py:112-222 (split-K with a deferred
+ * reduction has no counterpart in the reference).
+ */
+int cgpt_gemm_partials(const void* a, const void* w, float* partials, int64_t M, int64_t N,
+                       int64_t K, int64_t lda, int64_t ldw, int64_t ldp, int64_t n_split,
+                       int in_dtype, void* stream);
+
+/* The n_split cgpt_gemm_partials is tuned for at (M, N, K, in_dtype). */
+int cgpt_gemm_partials_plan(int64_t M, int64_t N, int64_t K, int in_dtype, int64_t* n_split);
 
 /*
  * Causal (or full) softmax attention, O = softmax(Q K^T * scale + mask) V,
@@ -179,8 +218,9 @@ int cgpt_embedding_at(const int64_t* idx, const void* wte, const void* wpe, void
  * step's key and value, (b, h, d) at base + b*sb + h*sh + d) into cache row
  * pos, then o = softmax(q K[0..pos]^T * scale) V[0..pos] — the causal row of
  * position pos.  P is rounded to `dtype` before the P*V product, as in
- * cgpt_attention_fwd.  head_dim divides 256 and is a multiple of 8 (bf16) / 4
- * (fp32); t_max <= 8192.  A device pos outside [0, t_max) is clamped and sets
+ * cgpt_attention_fwd.  head_dim is a power-of-two number (<= 32) of 16-byte
+ * vectors: 8..256 (bf16), 4..128 (fp32); t_max * c_st * element size < 2^31.
+ * A device pos outside [0, t_max) is clamped and sets
  * *err_flag.  Replaces the per-token full recompute of cutile_causal_attention
  * inside generate (cutile_gpt/models/gpt.py:185-229, attention.py:119-175).
  */
@@ -192,6 +232,26 @@ int cgpt_attention_decode(const void* q, const void* k_new, const void* v_new,
                           int64_t c_sb, int64_t c_sh, int64_t c_st, int64_t o_sb,
                           int64_t o_sh, float scale, int dtype, int* err_flag,
                           void* stream);
+
+/*
+ * cgpt_attention_decode with the step's q, k and v given as the fused QKV
+ * GEMM's split-K partial products (cgpt_gemm_partials over the c_attn weight):
+ * value d of head h of sequence b is column off + h*head_dim + d of
+ * P[0] + ... + P[n_parts-1] + qkv_bias (off = q_off / k_off / v_off; P[s] row
+ * b at qkv_partials + s * part_stride + b * ldp; qkv_bias of `dtype`), added
+ * in that order and rounded to `dtype` as the GEMM's output would be.
+ * 1 <= n_parts <= 16.  Other arguments as cgpt_attention_decode.  Replaces
+ * cutile_linear_bias on c_attn plus the attention of one generate step
+ * (cutile_gpt/models/gpt.py:124-146,185-229).
+ */
+int cgpt_attention_decode_partials(const float* qkv_partials, int64_t n_parts,
+                                   int64_t part_stride, int64_t ldp, const void* qkv_bias,
+                                   int64_t q_off, int64_t k_off, int64_t v_off, void* k_cache,
+                                   void* v_cache, void* o, int64_t B, int64_t H,
+                                   int64_t head_dim, int64_t t_max, int64_t pos_base,
+                                   const int* pos_dev, int64_t c_sb, int64_t c_sh, int64_t c_st,
+                                   int64_t o_sb, int64_t o_sh, float scale, int dtype,
+                                   int* err_flag, void* stream);
 
 /*
  * Copy T positions of keys and values ((b, h, t, d) at base + b*sb + h*sh + t*st
