@@ -19,27 +19,13 @@ namespace cgpt {
 // ------------------------------------------------------- decode attention
 
 constexpr int kDecThreads = 256;
+constexpr int kDecChunk = 256;  // keys per softmax chunk
 constexpr int kDecWaves = kDecThreads / 64;
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
   return v;
-}
-
-// Block-wide reduction of one value per thread (sum or max); `scr` holds
-// kDecWaves floats.  Every thread returns the result.
-template <bool kMax>
-__device__ __forceinline__ float block_reduce(float v, float* scr) {
-  v = kMax ? wave_max(v) : wave_sum(v);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  __syncthreads();
-  if (lane == 0) scr[wave] = v;
-  __syncthreads();
-  float r = scr[0];
-#pragma unroll
-  for (int w = 1; w < kDecWaves; ++w) r = kMax ? fmaxf(r, scr[w]) : r + scr[w];
-  return r;
 }
 
 template <typename T> __device__ __forceinline__ float round_to(float x);
@@ -62,7 +48,7 @@ struct DecIn {
   const T* bias;
 };
 
-// One block per (batch, head), keys in chunks of kDecThreads.  Thread
+// One block per (batch, head), keys in chunks of kDecChunk.  Thread
 // (kg, cv) = (tid / NV, tid % NV) owns 16-byte column vector cv of keys
 // kg, kg + KG, ... of a chunk for both K and V, so a wave's loads cover whole
 // cache rows; a chunk's K and V loads are all issued before the first is
@@ -70,21 +56,23 @@ struct DecIn {
 // and past pos read as zero: the new row comes from registers, and nothing is
 // read back from the cache rows this block writes).  Scores are dot products
 // reduced across the NV lanes of a key; softmax runs online across chunks
-// (one chunk for pos < kDecThreads).  P is rounded to T before the P V
-// product, as in the prefill kernel.
+// (one chunk for pos < kDecChunk), two barriers a chunk.  P is rounded to T
+// before the P V product, as in the prefill kernel.
 template <typename T, int NV, int MAXP>
-__global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(
+__global__ __launch_bounds__(kDecThreads, NV <= 8 ? 4 : 1) void attn_decode_kernel(
     DecIn<T> in, T* __restrict__ kc, T* __restrict__ vc, T* __restrict__ o, int H, int Tmax,
     int pos_base, const int* __restrict__ pos_dev, int64_t c_sb, int64_t c_sh, int64_t c_st,
     int64_t o_sb, int64_t o_sh, float scale_log2, int* err_flag) {
   constexpr int EPV = Elem<T>::kVec;  // elements per 16-byte vector
   constexpr int HD = NV * EPV;
-  constexpr int KG = kDecThreads / NV;  // keys per chunk a column lane visits: NV
+  constexpr int KG = kDecThreads / NV;   // key groups
+  constexpr int KPT = kDecChunk / KG;    // keys of a chunk per thread
+  constexpr int SPL = kDecChunk / 64;    // scores of a chunk per lane
   constexpr int R3 = (3 * HD + kDecThreads - 1) / kDecThreads;
+  static_assert(KPT >= 1, "head_dim too large for the chunk");
   __shared__ float qs[HD], kns[HD], vns[HD];
-  __shared__ float sc[kDecThreads];
+  __shared__ float sc[kDecChunk], pb[kDecChunk];
   __shared__ float part[KG][HD];
-  __shared__ float scr[kDecWaves];
   const int tid = threadIdx.x;
   const int kg = tid / NV, cv = tid % NV;
   const int b = blockIdx.x / H, h = blockIdx.x % H;
@@ -101,92 +89,97 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(vcb, 0, pos * row_bytes, 0x00020000);
 
   // The step's q / k / v values: thread tid + r * kDecThreads holds value i of
-  // the 3 * HD (q | k | v).
-  float sv[R3];
-  if (MAXP == 0) {
+  // the 3 * HD (q | k | v).  Their loads, then chunk 0's K and V loads, are
+  // all issued before the first is used.
+  float sv[R3], bv[R3];
+  float pv[R3][MAXP > 0 ? MAXP : 1];
+  const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(in.parts), 0, MAXP > 0 ? static_cast<int>(in.n_parts * in.part_stride * 4) : 0,
+      0x00020000);
 #pragma unroll
-    for (int r = 0; r < R3; ++r) {
-      const int i = tid + r * kDecThreads, which = i / HD, d = i % HD;
+  for (int r = 0; r < R3; ++r) {
+    const int i = tid + r * kDecThreads;
+    const int which = i < 3 * HD ? i / HD : 0, d = i % HD;
+    if (MAXP == 0) {
       const T* src = which == 0 ? in.q + b * in.q_sb + h * in.q_sh
                    : which == 1 ? in.kn + b * in.kn_sb + h * in.kn_sh
                                 : in.vn + b * in.vn_sb + h * in.vn_sh;
-      sv[r] = i < 3 * HD ? Elem<T>::load(src + d) : 0.f;
-    }
-  } else {
-    // Partials past n_parts lie past the record count and read as zero.
-    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(in.parts), 0, static_cast<int>(in.n_parts * in.part_stride * 4), 0x00020000);
-    float pv[R3][MAXP];
-#pragma unroll
-    for (int r = 0; r < R3; ++r) {
-      const int i = tid + r * kDecThreads, which = i / HD, d = i % HD;
+      sv[r] = Elem<T>::load(src + d);  // threads past 3 * HD load a valid element, unused
+    } else {
+      // Partials past n_parts lie past the record count and read as zero.
       const int64_t col = (which == 0 ? in.q_off : which == 1 ? in.k_off : in.v_off) + h * HD + d;
       const uint32_t off = static_cast<uint32_t>((b * in.ldp + col) * 4);
 #pragma unroll
       for (int s = 0; s < MAXP; ++s)
         pv[r][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-            rp, s < in.n_parts && i < 3 * HD ? off + static_cast<uint32_t>(s * in.part_stride * 4) : 0x80000000u,
-            0, 0));
-    }
-#pragma unroll
-    for (int r = 0; r < R3; ++r) {
-      const int i = tid + r * kDecThreads, which = i / HD, d = i % HD;
-      const int64_t col = (which == 0 ? in.q_off : which == 1 ? in.k_off : in.v_off) + h * HD + d;
-      float t = pv[r][0];
-#pragma unroll
-      for (int s = 1; s < MAXP; ++s)
-        if (s < in.n_parts) t += pv[r][s];
-      sv[r] = i < 3 * HD ? round_to<T>(t + Elem<T>::load(in.bias + col)) : 0.f;
+            rp, s < in.n_parts ? off + static_cast<uint32_t>(s * in.part_stride * 4) : 0x80000000u, 0, 0));
+      bv[r] = Elem<T>::load(in.bias + col);
     }
   }
+  u32x4_t kr[KPT], vr[KPT];
+  auto load_chunk = [&](int c0) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const uint32_t off = static_cast<uint32_t>((c0 + kg + KG * i) * row_bytes + cv * 16);
+      kr[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0);
+      vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
+    }
+  };
+  load_chunk(0);
+  if (MAXP > 0) {
+#pragma unroll
+    for (int r = 0; r < R3; ++r) {
+      // Slots past n_parts hold +0: adding them leaves every sum but -0 as is.
+      float t = pv[r][0];
+#pragma unroll
+      for (int s = 1; s < MAXP; ++s) t += pv[r][s];
+      sv[r] = round_to<T>(t + bv[r]);
+    }
+  }
+  // Publish q / k / v and append k, v at row pos of the cache.
+#pragma unroll
+  for (int r = 0; r < R3; ++r) {
+    const int i = tid + r * kDecThreads, which = i / HD, d = i % HD;
+    if (i < 3 * HD) {
+      if (which == 0) {
+        qs[d] = sv[r];
+      } else if (which == 1) {
+        kns[d] = sv[r];
+        Elem<T>::store(kcb + pos * c_st + d, sv[r]);
+      } else {
+        vns[d] = sv[r];
+        Elem<T>::store(vcb + pos * c_st + d, sv[r]);
+      }
+    }
+  }
+  __syncthreads();
+  float qv[EPV];
+#pragma unroll
+  for (int e = 0; e < EPV; ++e) qv[e] = qs[cv * EPV + e];
+  const int lane = tid & 63, wave = tid >> 6;
+  // The new key's score, reduced by every wave (the cache rows loaded above
+  // stop before row pos).
+  float sp = 0.f;
+  for (int d = lane; d < HD; d += 64) sp = fmaf(qs[d], kns[d], sp);
+  sp = wave_sum(sp) * scale_log2;
 
   float mrun = -INFINITY, lsum = 0.f;
   float acc[EPV];
 #pragma unroll
   for (int e = 0; e < EPV; ++e) acc[e] = 0.f;
 
-  for (int c0 = 0; c0 < Tk; c0 += kDecThreads) {
-    // This chunk's K and V vectors, all in flight together.
-    u32x4_t kr[NV], vr[NV];
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const uint32_t off = static_cast<uint32_t>((c0 + kg + KG * i) * row_bytes + cv * 16);
-      kr[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0);
-      vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
-    }
-    if (c0 == 0) {
-      // Publish q / k / v and append k, v at row pos of the cache.
-#pragma unroll
-      for (int r = 0; r < R3; ++r) {
-        const int i = tid + r * kDecThreads, which = i / HD, d = i % HD;
-        if (i < 3 * HD) {
-          if (which == 0) {
-            qs[d] = sv[r];
-          } else if (which == 1) {
-            kns[d] = sv[r];
-            Elem<T>::store(kcb + pos * c_st + d, sv[r]);
-          } else {
-            vns[d] = sv[r];
-            Elem<T>::store(vcb + pos * c_st + d, sv[r]);
-          }
-        }
-      }
-      __syncthreads();
-    }
-    float qv[EPV];
-#pragma unroll
-    for (int e = 0; e < EPV; ++e) qv[e] = qs[cv * EPV + e];
+  // Chunk c0 covers keys [c0, c0 + kDecChunk) of 0 .. pos; the last one
+  // holds the new key pos.
+  int c0 = 0;
+  for (;; c0 += kDecChunk) {
+    if (c0 > 0) load_chunk(c0);
     // Partial dot products of this lane's column vector, then summed over the
     // NV lanes of each key (consecutive lanes).
-    float s[NV];
+    float s[KPT];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
+    for (int i = 0; i < KPT; ++i) {
       float kv[EPV];
       unpack_vec<T>(kr[i], kv);
-      if (c0 + kg + KG * i == pos) {
-#pragma unroll
-        for (int e = 0; e < EPV; ++e) kv[e] = kns[cv * EPV + e];
-      }
       float t = 0.f;
 #pragma unroll
       for (int e = 0; e < EPV; ++e) t = fmaf(qv[e], kv[e], t);
@@ -195,35 +188,57 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(
 #pragma unroll
     for (int off = 1; off < NV; off <<= 1)
 #pragma unroll
-      for (int i = 0; i < NV; ++i) s[i] += __shfl_xor(s[i], off, 64);
+      for (int i = 0; i < KPT; ++i) s[i] += __shfl_xor(s[i], off, 64);
     if (cv == 0) {
 #pragma unroll
-      for (int i = 0; i < NV; ++i) sc[kg + KG * i] = s[i] * scale_log2;
+      for (int i = 0; i < KPT; ++i) {
+        const int j = kg + KG * i;
+        sc[j] = c0 + j == pos ? sp : s[i] * scale_log2;
+      }
     }
     __syncthreads();
-    const float sj = c0 + tid < Tk ? sc[tid] : -INFINITY;
-    const float mnew = fmaxf(mrun, block_reduce<true>(sj, scr));
+    // Every wave reduces the whole chunk (SPL scores a lane), so the chunk's
+    // maximum and sum need no further barrier; lane l of wave w < SPL also
+    // owns key 64 w + l's probability for the P V product.
+    float sj[SPL];
+    float cm = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < SPL; ++k) {
+      sj[k] = c0 + lane + 64 * k < Tk ? sc[lane + 64 * k] : -INFINITY;
+      cm = fmaxf(cm, sj[k]);
+    }
+    const float mnew = fmaxf(mrun, wave_max(cm));
     const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
-    const float p = c0 + tid < Tk ? __builtin_amdgcn_exp2f(sj - mnew) : 0.f;
-    lsum = lsum * alpha + block_reduce<false>(p, scr);
+    float ps = 0.f, pown = 0.f;
+#pragma unroll
+    for (int k = 0; k < SPL; ++k) {
+      const float p = c0 + lane + 64 * k < Tk ? __builtin_amdgcn_exp2f(sj[k] - mnew) : 0.f;
+      ps += p;
+      if (k == wave) pown = p;
+    }
+    lsum = lsum * alpha + wave_sum(ps);
     mrun = mnew;
-    sc[tid] = round_to<T>(p);  // sc[tid] was read by this thread only since the barrier
+    if (tid < kDecChunk) pb[tid] = round_to<T>(pown);
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < EPV; ++e) acc[e] *= alpha;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
+    for (int i = 0; i < KPT; ++i) {
       float vv[EPV];
-      unpack_vec<T>(vr[i], vv);
-      if (c0 + kg + KG * i == pos) {
-#pragma unroll
-        for (int e = 0; e < EPV; ++e) vv[e] = vns[cv * EPV + e];
-      }
-      const float pj = sc[kg + KG * i];
+      unpack_vec<T>(vr[i], vv);  // row pos reads as zero
+      const float pj = pb[kg + KG * i];
 #pragma unroll
       for (int e = 0; e < EPV; ++e) acc[e] = fmaf(pj, vv[e], acc[e]);
     }
-    __syncthreads();  // sc is rewritten by the next chunk
+    if (c0 + kDecChunk > pos) break;
+    // The next chunk's first barrier comes after this chunk's last read of
+    // pb and after every wave's reads of sc.
+  }
+  if (kg == 0) {
+    // The new value row, weighted by its probability from the last chunk.
+    const float pj = pb[pos - c0];
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) acc[e] = fmaf(pj, vns[cv * EPV + e], acc[e]);
   }
 #pragma unroll
   for (int e = 0; e < EPV; ++e) part[kg][cv * EPV + e] = acc[e];
@@ -327,7 +342,6 @@ static void launch_dec_nv(int nv, const DecIn<T>& in, T* kc, T* vc, T* o, int64_
                        o_sb, o_sh, sl2, err);                                                       \
     break;
   switch (nv) {
-    CGPT_DEC_NV(1)
     CGPT_DEC_NV(2)
     CGPT_DEC_NV(4)
     CGPT_DEC_NV(8)
@@ -348,9 +362,9 @@ static int check_decode(int64_t B, int64_t H, int64_t head_dim, int64_t t_max, i
   if (!k_cache || !v_cache || !o) return CGPT_EINVAL;
   if (dtype != CGPT_F32 && dtype != CGPT_BF16) return CGPT_EDTYPE;
   const int64_t es = dtype == CGPT_F32 ? 4 : 2, epv = 16 / es;
-  // head_dim = NV 16-byte vectors, NV a power of two dividing kDecThreads, at most 32.
+  // head_dim = NV 16-byte vectors, NV a power of two from 2 to 32.
   const int64_t nv = head_dim / epv;
-  if (head_dim % epv != 0 || nv > 32 || (nv & (nv - 1)) != 0) return CGPT_ESHAPE;
+  if (head_dim % epv != 0 || nv < 2 || nv > 32 || (nv & (nv - 1)) != 0) return CGPT_ESHAPE;
   if (B * H > 0x7fffffff || t_max > 0x7fffffff) return CGPT_ESHAPE;
   // Cache rows are read as 16-byte vectors through 32-bit buffer offsets.
   if (c_st % epv != 0 || c_sh % epv != 0 || c_sb % epv != 0 || c_st < head_dim) return CGPT_EINVAL;

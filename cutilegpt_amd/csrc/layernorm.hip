@@ -226,10 +226,10 @@ __global__ __launch_bounds__(kLnpThreads) void add_layernorm_partials_kernel(
     decode_param(biraw[c], param_bf16, bi[c]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      // Slots past n_parts hold +0: adding them leaves every sum but -0 as is.
       float d = __uint_as_float(praw[c][0][j]);
 #pragma unroll
-      for (int s = 1; s < MAXP; ++s)
-        if (s < n_parts) d += __uint_as_float(praw[c][s][j]);
+      for (int s = 1; s < MAXP; ++s) d += __uint_as_float(praw[c][s][j]);
       const float t = v[c][j] + round_delta<TD>(d + bi[c][j]);
       v[c][j] = ok ? t : 0.f;
       sum += v[c][j];

@@ -150,10 +150,13 @@ class DecodeSession:
         pws, pcnt, nws, ncnt = (self.ws.data_ptr(), self.counters.data_ptr(), self.ws_bytes,
                                 self.counters.numel())
 
-        def gemm(a_ptr, w, b, c_ptr, n, k, epi, out_code):
+        def gemm(a_ptr, w, b, c_ptr, n, k, epi, out_code, split=True):
+            # split=False: the unsplit kernel, whose wider blocks suit the wide
+            # GEMMs (c_fc, the LM head) better than the cross-block fix-up.
             chk(lib.cgpt_gemm_skinny(a_ptr, w.data_ptr(), None if b is None else b.data_ptr(),
                                      c_ptr, B, n, k, k, w.stride(0), n, ac, ac, out_code, epi,
-                                     pws, nws, pcnt, ncnt, s), "gemm_skinny")
+                                     pws if split else None, nws, pcnt if split else None, ncnt,
+                                     s), "gemm_skinny")
 
         def add_ln(delta_ptr, wk, keep_x=True):
             chk(lib.cgpt_add_layernorm(px, delta_ptr, px if delta_ptr and keep_x else None,
@@ -196,7 +199,7 @@ class DecodeSession:
                 ns = gemm_parts(pa, W[p + "attn.c_proj.weight"], D, D)
                 add_ln_parts(ns, W[p + "attn.c_proj.bias"], p + "ln_2")
                 gemm(ph, W[p + "mlp.c_fc.weight"], W[p + "mlp.c_fc.bias"], pf, 4 * D, D,
-                     _lib.EPI_BIAS_GELU, ac)
+                     _lib.EPI_BIAS_GELU, ac, split=False)
                 ns = gemm_parts(pf, W[p + "mlp.c_proj.weight"], D, 4 * D)
                 add_ln_parts(ns, W[p + "mlp.c_proj.bias"], ln_next, keep_x=not last)
                 continue
@@ -216,7 +219,7 @@ class DecodeSession:
                  _lib.EPI_BIAS, ac)
             add_ln(pd, ln_next, keep_x=not last)
         gemm(ph, W["lm_head.weight"], None, self.logits.data_ptr(), V, D, _lib.EPI_NONE,
-             _DT[self.logits.dtype])
+             _DT[self.logits.dtype], split=not self.partials)
 
     def greedy_step(self) -> None:
         """``step_logits`` + argmax into ``ids`` and history column step + 1,

@@ -218,8 +218,9 @@ int cgpt_embedding_at(const int64_t* idx, const void* wte, const void* wpe, void
  * step's key and value, (b, h, d) at base + b*sb + h*sh + d) into cache row
  * pos, then o = softmax(q K[0..pos]^T * scale) V[0..pos] — the causal row of
  * position pos.  P is rounded to `dtype` before the P*V product, as in
- * cgpt_attention_fwd.  head_dim is a power-of-two number (<= 32) of 16-byte
- * vectors: 8..256 (bf16), 4..128 (fp32); t_max * c_st * element size < 2^31.
+ * cgpt_attention_fwd.  head_dim is a power-of-two number (2 to 32) of
+ * 16-byte vectors: 16..256 (bf16), 8..128 (fp32); t_max * c_st * element
+ * size < 2^31.
  * A device pos outside [0, t_max) is clamped and sets
  * *err_flag.  Replaces the per-token full recompute of cutile_causal_attention
  * inside generate (cutile_gpt/models/gpt.py:185-229, attention.py:119-175).
