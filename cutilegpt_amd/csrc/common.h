@@ -90,12 +90,42 @@ __device__ __forceinline__ void store_vec(bf16_t* p, const float* in) {
   *reinterpret_cast<u32x4_t*>(p) = v;
 }
 
-// Butterfly sum / max across the 64 lanes of a wavefront.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+// Cross-lane reductions through DPP (VALU operand modifiers, no LDS round
+// trip as with __shfl_xor's ds_bpermute).  kDppXor1 / kDppXor2 swap
+// neighbours within quads; kDppMirror8 pairs lane i with 7 - i of its group
+// of 8, kDppMirror16 with 15 - i of its row of 16 — after xor1, xor2 and
+// mirror8 each lane of an 8-lane group has combined all 8.
+template <int CTRL> __device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppMirror8 = 0x141, kDppMirror16 = 0x140;
+__device__ __forceinline__ float lane_value(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// Sum over groups of G consecutive lanes (G = 1, 2, 4, 8 or 16), in every lane.
+template <int G> __device__ __forceinline__ float group_sum(float v) {
+  if (G >= 2) v += dpp<kDppXor1>(v);
+  if (G >= 4) v += dpp<kDppXor2>(v);
+  if (G >= 8) v += dpp<kDppMirror8>(v);
+  if (G >= 16) v += dpp<kDppMirror16>(v);
   return v;
 }
+
+// Max / sum over the 64 lanes: rows of 16 through DPP, then the 4 rows'
+// results read back as scalars (the same value in every lane).
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp<kDppXor1>(v));
+  v = fmaxf(v, dpp<kDppXor2>(v));
+  v = fmaxf(v, dpp<kDppMirror8>(v));
+  v = fmaxf(v, dpp<kDppMirror16>(v));
+  return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v = group_sum<16>(v);
+  return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+
 
 // tanh-approximate GELU written through the identity
 //   0.5 x (1 + tanh(u)) = x / (1 + exp(-2u)),  u = sqrt(2/pi) (x + 0.044715 x^3),

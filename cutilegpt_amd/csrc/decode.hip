@@ -22,10 +22,12 @@ constexpr int kDecThreads = 256;
 constexpr int kDecChunk = 256;  // keys per softmax chunk
 constexpr int kDecWaves = kDecThreads / 64;
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+// Barrier for LDS traffic only: the block's LDS writes are complete, its
+// global stores (the cache append) may still be in flight.  __syncthreads()
+// would also wait for those stores' write acknowledgements.
+__device__ __forceinline__ void lds_barrier() {
+  wait_lgkm0();
+  raw_barrier();
 }
 
 template <typename T> __device__ __forceinline__ float round_to(float x);
@@ -125,6 +127,9 @@ __global__ __launch_bounds__(kDecThreads, NV <= 8 ? 4 : 1) void attn_decode_kern
       vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
     }
   };
+  // Keep the q / k / v loads ahead of the K and V loads: vmcnt retires in
+  // issue order, so their sums then wait for them alone.
+  __builtin_amdgcn_sched_barrier(0);
   load_chunk(0);
   if (MAXP > 0) {
 #pragma unroll
@@ -152,7 +157,7 @@ __global__ __launch_bounds__(kDecThreads, NV <= 8 ? 4 : 1) void attn_decode_kern
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
   float qv[EPV];
 #pragma unroll
   for (int e = 0; e < EPV; ++e) qv[e] = qs[cv * EPV + e];
@@ -185,10 +190,15 @@ __global__ __launch_bounds__(kDecThreads, NV <= 8 ? 4 : 1) void attn_decode_kern
       for (int e = 0; e < EPV; ++e) t = fmaf(qv[e], kv[e], t);
       s[i] = t;
     }
+    if constexpr (NV <= 16) {
 #pragma unroll
-    for (int off = 1; off < NV; off <<= 1)
+      for (int i = 0; i < KPT; ++i) s[i] = group_sum<NV>(s[i]);
+    } else {
 #pragma unroll
-      for (int i = 0; i < KPT; ++i) s[i] += __shfl_xor(s[i], off, 64);
+      for (int off = 1; off < NV; off <<= 1)
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) s[i] += __shfl_xor(s[i], off, 64);
+    }
     if (cv == 0) {
 #pragma unroll
       for (int i = 0; i < KPT; ++i) {
@@ -196,7 +206,7 @@ __global__ __launch_bounds__(kDecThreads, NV <= 8 ? 4 : 1) void attn_decode_kern
         sc[j] = c0 + j == pos ? sp : s[i] * scale_log2;
       }
     }
-    __syncthreads();
+    lds_barrier();
     // Every wave reduces the whole chunk (SPL scores a lane), so the chunk's
     // maximum and sum need no further barrier; lane l of wave w < SPL also
     // owns key 64 w + l's probability for the P V product.
@@ -219,7 +229,7 @@ __global__ __launch_bounds__(kDecThreads, NV <= 8 ? 4 : 1) void attn_decode_kern
     lsum = lsum * alpha + wave_sum(ps);
     mrun = mnew;
     if (tid < kDecChunk) pb[tid] = round_to<T>(pown);
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int e = 0; e < EPV; ++e) acc[e] *= alpha;
 #pragma unroll
@@ -242,7 +252,7 @@ __global__ __launch_bounds__(kDecThreads, NV <= 8 ? 4 : 1) void attn_decode_kern
   }
 #pragma unroll
   for (int e = 0; e < EPV; ++e) part[kg][cv * EPV + e] = acc[e];
-  __syncthreads();
+  lds_barrier();
   for (int d = tid; d < HD; d += kDecThreads) {
     float t = 0.f;
     for (int k = 0; k < KG; ++k) t += part[k][d];
