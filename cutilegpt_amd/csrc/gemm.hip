@@ -1377,7 +1377,15 @@ static int launch_tile(int tile, const void* a, const void* w, const void* bias,
 // Default tile choice when the caller's table has no entry: the register-staged
 // kernel with the largest tile that still gives every CU about two blocks
 // (128x128 for long K, 128x64 otherwise), smaller tiles for small grids.
-static int auto_tile(bool bf16, int M, int N, int K) {
+static int auto_tile(bool bf16, int M, int N, int K, int64_t lda, int64_t ldw) {
+  // Problems with at least one 256x192 tile per CU: the persistent
+  // direct-to-LDS pipelines (256x256 with wave-staged stores for wide N, as
+  // the LM heads measured best; 256x192 with block-staged stores otherwise).
+  if (bf16) {
+    const int64_t tiles = static_cast<int64_t>((M + 255) / 256) * ((N + 191) / 192);
+    const int pick = N >= 16384 ? 15 : 14;
+    if (tiles >= 256 && pipe_ok(pick, M, N, K, lda, ldw)) return pick;
+  }
   const TileCfg* t = bf16 ? kBf16Tiles : kF32Tiles;
   const int nt = bf16 ? kNumBf16Tiles : kNumF32Tiles;
   const int first = bf16 ? (K >= 2048 ? 2 : 3) : 0;
@@ -1508,7 +1516,7 @@ extern "C" int cgpt_gemm(const void* a, const void* w, const void* bias, void* c
                               static_cast<hipStream_t>(stream));
   }
   if (tile == CGPT_TILE_AUTO)
-    tile = auto_tile(bf16, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K));
+    tile = auto_tile(bf16, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), lda, ldw);
   if (tile < 0 || tile >= nt) return CGPT_EINVAL;
   if (bf16 && tile >= kFirstPipeTile && !pipe_ok(tile, M, N, K, lda, ldw)) return CGPT_ESHAPE;
   const int64_t out_align = out_dtype == CGPT_F32 ? 16 : 8;
