@@ -1,6 +1,6 @@
 """Prefill throughput of the GPT-2 forward hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload gpt2|medium|xl-decode]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload gpt2|medium|xl-decode|kernels]
 
 Workload (default): GPT-2 124M architecture (12 layers, 12 heads, d 768, MLP 3072,
 vocab 50257), bf16 random-init weights N(0, 0.02) written as an HF GPT-2
@@ -15,6 +15,11 @@ steps.  ``cpu_baseline`` is the CPU oracle's fp32 forward of the same model
 (a minGPT-architecture PyTorch forward) on the host cores, over a bounded
 sample.  ``breakdown`` comes from one extra, separately timed forward with
 events around every launch.
+
+``standalone_kernels`` (also ``--workload kernels`` on its own): the standalone
+kernel set — tanh-GELU, LayerNorm and causal attention in fp32 and bf16 — each
+timed over rotating buffers larger than the MALL, as a fraction of its
+roofline.
 
 ``--workload xl-decode``: KV-cache greedy decoding of GPT-2 XL (48 layers, 25
 heads, d 1600), bf16 N(0, 0.02) weights generated on the device, batch 32,
@@ -68,7 +73,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="gpt2", choices=sorted(WORKLOADS) + ["xl-decode"])
+    ap.add_argument("--workload", default="gpt2", choices=sorted(WORKLOADS) + ["xl-decode", "kernels"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seqs", type=int, default=2,
                     help="sequences (of seq_len tokens) per timed CPU-baseline forward")
@@ -84,6 +89,9 @@ def main():
 
     if args.workload == "xl-decode":
         bench_xl_decode(args)
+        return
+    if args.workload == "kernels":
+        bench_kernels(args)
         return
 
     import torch
@@ -194,6 +202,9 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    # The standalone kernel set (GELU / LayerNorm / attention, fp32 and bf16).
+    standalone = standalone_kernels() if args.workload == "gpt2" else None
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(w, ids, H, args.cpu_seqs)
@@ -221,6 +232,7 @@ def main():
                      "avg_launch_ms": round(head_avg_ms, 4)},
         "forward_tflops": round((gemm_f + head_f + attn_f) / (ms_per_step * 1e-3) / 1e12, 1),
         "breakdown": breakdown,
+        "standalone_kernels": standalone,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
@@ -345,6 +357,119 @@ def bench_xl_decode(args):
                      "lm_head_skinny": {"avg_launch_ms": round(head_ms, 4),
                                         "achieved_GBs": round(head_bytes / head_ms / 1e6, 1),
                                         "frac": round(head_bytes / head_ms / 1e6 / PEAK_HBM_GBS, 4)}},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
+
+PEAK_FP32_TFLOPS = 157.3    # MI355X dense fp32 MFMA
+# Rotating working set of the HBM-bound standalone kernels: several times the
+# 256 MB MALL, so every launch streams from and to HBM.
+ROTATE_BYTES = 640 << 20
+
+
+def standalone_kernels(iters=40):
+    """The standalone kernel set (tanh-GELU on 32x512x768, LayerNorm over 16384
+    rows of 768 with gamma~N(1,0.1), beta~N(0,0.1), causal attention 12 heads x
+    64 at batch 8 x seq 512), fp32 and bf16, inputs N(0,1) from seed 0.  Each
+    kernel is launched ``iters`` times through the C ABI between two HIP events
+    on the launch stream; GELU and LayerNorm rotate over copies of their
+    buffers totalling ~ROTATE_BYTES so no launch reads what an earlier one left
+    in the MALL.  Returns {name: {...}} with the average launch time and the
+    achieved fraction of the kernel's roofline (HBM for GELU/LN, MFMA for
+    attention)."""
+    import torch
+    from cutilegpt_amd import _lib
+
+    lib = _lib.load()
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream(dev)
+    s = st.cuda_stream
+    code = {torch.float32: _lib.CGPT_F32, torch.bfloat16: _lib.CGPT_BF16}
+
+    def timed(launch, nbuf):
+        for i in range(nbuf):
+            launch(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for i in range(iters):
+            launch(i % nbuf)
+        e1.record(st)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters
+
+    def copies(t, pair_bytes):
+        n = max(2, -(-ROTATE_BYTES // pair_bytes))
+        return [t.clone() for _ in range(n)]
+
+    g = torch.Generator().manual_seed(0)
+    gelu_x = torch.randn(32, 512, 768, generator=g)
+    ln_x = torch.randn(16384, 768, generator=g)
+    ln_w = 1.0 + 0.1 * torch.randn(768, generator=g)
+    ln_b = 0.1 * torch.randn(768, generator=g)
+    qkv = [torch.randn(8, 12, 512, 64, generator=g) for _ in range(3)]
+    out = {}
+    for dt, tag in ((torch.float32, "fp32"), (torch.bfloat16, "bf16")):
+        es = torch.finfo(dt).bits // 8
+        # GELU: read n + write n elements.
+        n = gelu_x.numel()
+        xs = copies(gelu_x.to(dev, dt), 2 * n * es)
+        ys = [torch.empty_like(xs[0]) for _ in xs]
+        ms = timed(lambda i: _lib.check(lib.cgpt_gelu(xs[i].data_ptr(), ys[i].data_ptr(), n,
+                                                      code[dt], s), "gelu"), len(xs))
+        nbytes = 2 * n * es
+        out[f"gelu_{tag}"] = {"shape": [32, 512, 768], "avg_launch_ms": round(ms, 4),
+                              "bytes": nbytes, "GB/s": round(nbytes / ms / 1e6, 1),
+                              "frac": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4), "bound": "hbm"}
+        del xs, ys
+        # LayerNorm: read x, write y, read gamma and beta.
+        M, N = ln_x.shape
+        xs = copies(ln_x.to(dev, dt), 2 * M * N * es)
+        ys = [torch.empty_like(xs[0]) for _ in xs]
+        gw, gb = ln_w.to(dev, dt), ln_b.to(dev, dt)
+        ms = timed(lambda i: _lib.check(lib.cgpt_add_layernorm(
+            xs[i].data_ptr(), None, None, gw.data_ptr(), gb.data_ptr(), ys[i].data_ptr(), M, N,
+            1e-5, code[dt], 0, code[dt], code[dt], s), "layernorm"), len(xs))
+        nbytes = 2 * M * N * es + 2 * N * es
+        out[f"layernorm_{tag}"] = {"shape": [M, N], "avg_launch_ms": round(ms, 4),
+                                   "bytes": nbytes, "GB/s": round(nbytes / ms / 1e6, 1),
+                                   "frac": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4),
+                                   "bound": "hbm"}
+        del xs, ys
+        # Causal attention, (B, H, T, hd) contiguous: 4*B*H*hd*T(T+1)/2 FLOP.
+        B, H, T, hd = qkv[0].shape
+        q, k, v = (t.to(dev, dt) for t in qkv)
+        o = torch.empty_like(q)
+        qs = q.stride()[:3]
+        ms = timed(lambda i: _lib.check(lib.cgpt_attention_fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), B, H, T, T, hd, *qs, *qs,
+            *qs, *qs, 1.0 / math.sqrt(hd), 1, code[dt], s), "attention"), 1)
+        fl = 4 * B * H * hd * T * (T + 1) // 2
+        peak = PEAK_FP32_TFLOPS if dt == torch.float32 else PEAK_BF16_TFLOPS
+        out[f"attention_{tag}"] = {"shape": [B, H, T, hd], "avg_launch_ms": round(ms, 4),
+                                   "flop": fl, "TFLOP/s": round(fl / ms / 1e9, 1),
+                                   "frac": round(fl / ms / 1e9 / peak, 4), "bound": "mfma",
+                                   "peak_TFLOP/s": peak}
+        del q, k, v, o
+    torch.cuda.synchronize()
+    return out
+
+
+def bench_kernels(args):
+    """``--workload kernels``: the standalone kernel set alone, one JSON line."""
+    res = standalone_kernels(iters=max(args.steps, 10))
+    fracs = [r["frac"] for r in res.values()]
+    line = {
+        "metric": "standalone kernel set (tanh-GELU 32x512x768, LayerNorm 16384x768, causal "
+                  "attention b8 h12 s512 d64; fp32 and bf16): fraction of roofline",
+        "value": round(sum(fracs) / len(fracs), 4),
+        "unit": "mean frac of roofline over the 6 kernels",
+        "n_gpus": 1, "steps": max(args.steps, 10), "warmup": 1,
+        "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32+bf16", "data": "synthetic N(0,1) inputs from seed 0",
+        "config": {"workload": "standalone kernels", "rotate_bytes": ROTATE_BYTES},
+        "kernels": res,
         "cpu_baseline": None,
     }
     print(json.dumps(line), flush=True)

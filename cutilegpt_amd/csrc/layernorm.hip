@@ -1,11 +1,14 @@
-// Fused residual add + LayerNorm (HBM-bound, one wavefront per row).
+// Fused residual add + LayerNorm (HBM-bound, rows held in registers).
 //
-// A 256-thread block normalises 4 rows.  Lane l of a wave owns columns
-// [4(64c + l), 4(64c + l) + 4) for chunk c < ceil(cols / 256), so every load and
-// store of a wave covers one contiguous 1 KiB (fp32) or 512 B (bf16) span.  The
-// whole row stays in registers: mean and the centred variance are two
-// butterfly reductions over the registers (no second read of x), the residual
-// sum is written once (x_out) and the normalised row once (y).
+// A 256-thread block is 4 waves; a wave normalises R consecutive rows.  Lane l
+// owns columns [4(64c + l), 4(64c + l) + 4) of each row for chunk c <
+// ceil(cols / 256), so every load and store of a wave covers one contiguous
+// 1 KiB (fp32) or 512 B (bf16) span.  Whole rows stay in registers: mean and
+// the centred variance are two wave reductions over the registers (no second
+// read of x), the residual sum is written once (x_out) and the normalised row
+// once (y).
+#include <type_traits>
+
 #include "common.h"
 
 namespace cgpt {
@@ -27,6 +30,34 @@ __device__ __forceinline__ void store4(bf16_t* p, const float* v) {
   *reinterpret_cast<u32x2_t*>(p) = u;
 }
 
+// The same four elements through non-temporal (streaming) accesses: the
+// lines are marked for early eviction instead of being kept for reuse.
+__device__ __forceinline__ void load4_nt(const float* p, float* v) {
+  const f32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(p));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = t[j];
+}
+__device__ __forceinline__ void load4_nt(const bf16_t* p, float* v) {
+  const u32x2_t u = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+  v[0] = __uint_as_float(u[0] << 16);
+  v[1] = __uint_as_float(u[0] & 0xffff0000u);
+  v[2] = __uint_as_float(u[1] << 16);
+  v[3] = __uint_as_float(u[1] & 0xffff0000u);
+}
+__device__ __forceinline__ void store4_nt(float* p, const float* v) {
+  __builtin_nontemporal_store(f32x4_t{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4_t*>(p));
+}
+__device__ __forceinline__ void store4_nt(bf16_t* p, const float* v) {
+  __builtin_nontemporal_store(u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])},
+                              reinterpret_cast<u32x2_t*>(p));
+}
+template <bool NT, typename T> __device__ __forceinline__ void load4p(const T* p, float* v) {
+  if constexpr (NT) load4_nt(p, v); else load4(p, v);
+}
+template <bool NT, typename T> __device__ __forceinline__ void store4p(T* p, const float* v) {
+  if constexpr (NT) store4_nt(p, v); else store4(p, v);
+}
+
 // gamma / beta: 16 raw bytes from the chunk's first element through a buffer
 // resource (fp32: 4 values; bf16: the first 8 bytes), decoded by the uniform
 // type flag after the load, so no branch separates a load from its use.
@@ -42,103 +73,147 @@ __device__ __forceinline__ void decode_param(u32x4_t r, bool bf16, float* v) {
   }
 }
 
-template <typename TX, typename TD, typename TY, int MAXCH>
+// R rows per wave, NCH 256-column chunks per row (the smallest count that
+// covers it, so no load slot is wasted on a padded chunk); POL bit 0 makes the
+// x / delta loads non-temporal, bit 1 the x_out / y stores.  Every load of the wave's rows is issued before
+// any is used, with no branch around them: columns past the row load column
+// 0 and rows past the last load the last row, both masked — one memory round
+// trip per wave, which is what short batches (decode steps) are bound by.
+template <typename TX, typename TD, typename TY, int NCH, int R, bool HASD, int POL>
 __global__ __launch_bounds__(kLnThreads) void add_layernorm_kernel(
     const TX* __restrict__ x, const TD* __restrict__ delta, TX* x_out,
     const void* __restrict__ gamma, const void* __restrict__ beta, bool param_bf16,
     TY* __restrict__ y, int64_t rows, int cols, float eps) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kLnRowsPerBlock + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const int64_t base = row * cols;
+  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kLnRowsPerBlock + (threadIdx.x >> 6)) * R;
+  if (row0 >= rows) return;
   const int pshift = param_bf16 ? 1 : 2;
   const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<void*>(gamma), 0, cols << pshift, 0x00020000);
   const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<void*>(beta), 0, cols << pshift, 0x00020000);
 
-  // Every load of the row is issued before any is used, with no branch around
-  // it: columns past the row load column 0 and are masked, so the wave's
-  // loads (x, delta, gamma, beta) are in flight together — one memory round
-  // trip, which is what short batches (decode steps) are bound by.
-  // Without delta the x row is loaded a second time in its place (same bytes,
-  // discarded by a select), so the loads stay unconditional.
-  const bool has_delta = delta != nullptr;
-  const TD* dsrc = has_delta ? delta : reinterpret_cast<const TD*>(x);
-  const int64_t dbase = has_delta ? base : 0;
-  float v[MAXCH][4], dv[MAXCH][4], gm[MAXCH][4], bt[MAXCH][4];
-  u32x4_t graw[MAXCH], braw[MAXCH];
-  float sum = 0.f;
+  float v[R][NCH][4], dv[R][NCH][4];
+  u32x4_t graw[NCH], braw[NCH];
 #pragma unroll
-  for (int c = 0; c < MAXCH; ++c) {
-    const int col = (c * 64 + lane) * 4;
-    const int cc = col < cols ? col : 0;
-    load4(x + base + cc, v[c]);
-    load4(dsrc + dbase + (has_delta ? cc : 0), dv[c]);
-    graw[c] = __builtin_amdgcn_raw_buffer_load_b128(rg, cc << pshift, 0, 0);
-    braw[c] = __builtin_amdgcn_raw_buffer_load_b128(rb, cc << pshift, 0, 0);
+  for (int i = 0; i < R; ++i) {
+    const int64_t base = min(row0 + i, rows - 1) * cols;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int col = (c * 64 + lane) * 4;
+      const int cc = col < cols ? col : 0;
+      load4p<(POL & 1) != 0>(x + base + cc, v[i][c]);
+      if constexpr (HASD) load4p<(POL & 1) != 0>(delta + base + cc, dv[i][c]);
+    }
   }
 #pragma unroll
-  for (int c = 0; c < MAXCH; ++c) {
-    const bool ok = (c * 64 + lane) * 4 < cols;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float t = v[c][j] + (has_delta ? dv[c][j] : 0.f);
-      v[c][j] = ok ? t : 0.f;
-      sum += v[c][j];
-    }
-    decode_param(graw[c], param_bf16, gm[c]);
-    decode_param(braw[c], param_bf16, bt[c]);
+  for (int c = 0; c < NCH; ++c) {
+    const int col = (c * 64 + lane) * 4;
+    const int cc = col < cols ? col : 0;
+    graw[c] = __builtin_amdgcn_raw_buffer_load_b128(rg, cc << pshift, 0, 0);
+    braw[c] = __builtin_amdgcn_raw_buffer_load_b128(rb, cc << pshift, 0, 0);
   }
   // Correctly rounded divisions (not a multiply by 1/cols, which the compiler
   // may fuse into x - mean): a constant row then gives mean == x exactly and
   // y == beta.
   const float n_f = static_cast<float>(cols);
-  const float mean = wave_sum(sum) / n_f;
-  float sq = 0.f;
+  float mean[R], rstd[R];
 #pragma unroll
-  for (int c = 0; c < MAXCH; ++c) {
-    const bool ok = (c * 64 + lane) * 4 < cols;
+  for (int i = 0; i < R; ++i) {
+    float sum = 0.f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float t = v[c][j] - mean;
-      sq += ok ? t * t : 0.f;
+    for (int c = 0; c < NCH; ++c) {
+      const bool ok = (c * 64 + lane) * 4 < cols;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float t = HASD ? v[i][c][j] + dv[i][c][j] : v[i][c][j];
+        v[i][c][j] = ok ? t : 0.f;
+        sum += v[i][c][j];
+      }
     }
+    mean[i] = wave_sum(sum) / n_f;
   }
-  const float var = wave_sum(sq) / n_f;
-  const float rstd = 1.0f / sqrtf(var + eps);
 #pragma unroll
-  for (int c = 0; c < MAXCH; ++c) {
+  for (int i = 0; i < R; ++i) {
+    float sq = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const bool ok = (c * 64 + lane) * 4 < cols;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float t = v[i][c][j] - mean[i];
+        sq += ok ? t * t : 0.f;
+      }
+    }
+    rstd[i] = 1.0f / sqrtf(wave_sum(sq) / n_f + eps);
+  }
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    float gm[4], bt[4];
+    decode_param(graw[c], param_bf16, gm);
+    decode_param(braw[c], param_bf16, bt);
     const int col = (c * 64 + lane) * 4;
-    if (col < cols) {
-      if (x_out != nullptr) store4(x_out + base + col, v[c]);
-      float o[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) o[j] = (v[c][j] - mean) * rstd * gm[c][j] + bt[c][j];
-      store4(y + base + col, o);
+    for (int i = 0; i < R; ++i) {
+      if (col < cols && row0 + i < rows) {
+        const int64_t base = (row0 + i) * cols;
+        if (x_out != nullptr) store4p<(POL & 2) != 0>(x_out + base + col, v[i][c]);
+        float o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = (v[i][c][j] - mean[i]) * rstd[i] * gm[j] + bt[j];
+        store4p<(POL & 2) != 0>(y + base + col, o);
+      }
     }
   }
+}
+
+template <typename TX, typename TD, typename TY, int NCH, bool HASD>
+static void launch_ln_nch(const TX* x, const TD* d, TX* xo, const void* gamma, const void* beta,
+                          bool pb, TY* y, int64_t rows, int cols, float eps, hipStream_t s) {
+  // One row per wave: with 2 or 4 rows a wave (fewer, longer waves) the
+  // 16384-row GPT-2 batch ran 4-15 % slower.  Streaming policy, from a sweep
+  // over rotating buffers larger than the MALL: with a delta (the model's
+  // residual add), non-temporal loads and cached stores (the next GEMM reads
+  // y right away); without one, non-temporal loads and stores.
+  constexpr int R = 1, POL = HASD ? 1 : 3;
+  const dim3 grid(static_cast<unsigned>((rows + kLnRowsPerBlock * R - 1) / (kLnRowsPerBlock * R)));
+  hipLaunchKernelGGL((add_layernorm_kernel<TX, TD, TY, NCH, R, HASD, POL>), grid, dim3(kLnThreads), 0, s,
+                     x, d, xo, gamma, beta, pb, y, rows, cols, eps);
+}
+
+template <typename TX, typename TD, typename TY, bool HASD>
+static void launch_ln_cols(const TX* x, const TD* d, TX* xo, const void* gamma, const void* beta,
+                           bool pb, TY* y, int64_t rows, int cols, float eps, hipStream_t s) {
+  if (cols <= 512)
+    launch_ln_nch<TX, TD, TY, 2, HASD>(x, d, xo, gamma, beta, pb, y, rows, cols, eps, s);
+  else if (cols <= 768)
+    launch_ln_nch<TX, TD, TY, 3, HASD>(x, d, xo, gamma, beta, pb, y, rows, cols, eps, s);
+  else if (cols <= 1024)
+    launch_ln_nch<TX, TD, TY, 4, HASD>(x, d, xo, gamma, beta, pb, y, rows, cols, eps, s);
+  else if (cols <= 1792)
+    launch_ln_nch<TX, TD, TY, 7, HASD>(x, d, xo, gamma, beta, pb, y, rows, cols, eps, s);
+  else if (cols <= 2048)
+    launch_ln_nch<TX, TD, TY, 8, HASD>(x, d, xo, gamma, beta, pb, y, rows, cols, eps, s);
+  else
+    launch_ln_nch<TX, TD, TY, 16, HASD>(x, d, xo, gamma, beta, pb, y, rows, cols, eps, s);
 }
 
 template <typename TX, typename TD, typename TY>
 static int launch_ln3(const void* x, const void* delta, void* x_out, const void* gamma,
                       const void* beta, bool param_bf16, void* y, int64_t rows, int cols,
                       float eps, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>((rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock));
-  const dim3 block(kLnThreads);
   const TX* xp = static_cast<const TX*>(x);
   const TD* dp = static_cast<const TD*>(delta);
   TX* xo = static_cast<TX*>(x_out);
   TY* yp = static_cast<TY*>(y);
-  if (cols <= 1024)
-    hipLaunchKernelGGL((add_layernorm_kernel<TX, TD, TY, 4>), grid, block, 0, s, xp, dp, xo, gamma,
-                       beta, param_bf16, yp, rows, cols, eps);
-  else if (cols <= 2048)
-    hipLaunchKernelGGL((add_layernorm_kernel<TX, TD, TY, 8>), grid, block, 0, s, xp, dp, xo, gamma,
-                       beta, param_bf16, yp, rows, cols, eps);
-  else
-    hipLaunchKernelGGL((add_layernorm_kernel<TX, TD, TY, 16>), grid, block, 0, s, xp, dp, xo,
-                       gamma, beta, param_bf16, yp, rows, cols, eps);
+  if (dp != nullptr) {
+    launch_ln_cols<TX, TD, TY, true>(xp, dp, xo, gamma, beta, param_bf16, yp, rows, cols, eps, s);
+  } else if constexpr (std::is_same<TX, TD>::value) {
+    // Without a delta the TD parameter is unused: only the TD = TX instance exists.
+    launch_ln_cols<TX, TD, TY, false>(xp, dp, xo, gamma, beta, param_bf16, yp, rows, cols, eps, s);
+  } else {
+    return CGPT_EINVAL;
+  }
   return hip_status(hipGetLastError());
 }
 

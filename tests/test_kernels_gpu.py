@@ -38,7 +38,7 @@ def close(out, ref, atol, rtol, what=""):
 # --------------------------------------------------------------------- GELU
 
 @pytest.mark.parametrize("dtype", [F32, BF16])
-@pytest.mark.parametrize("n", [1, 7, 4099, 32 * 512 * 768])
+@pytest.mark.parametrize("n", [1, 7, 4099, 8200, (1 << 20) + 24, 32 * 512 * 768])
 def test_gelu(gpu, dtype, n):
     x = randn(n, seed=n, dtype=dtype)
     y = cg.cutile_gelu(x.to(gpu))
@@ -58,7 +58,8 @@ def test_gelu_3d_shape_and_special_values(gpu):
 
 # ---------------------------------------------------------------- LayerNorm
 
-@pytest.mark.parametrize("rows,cols", [(1, 4), (5, 48), (37, 768), (3, 1600), (7, 4096),
+@pytest.mark.parametrize("rows,cols", [(1, 4), (5, 48), (2, 512), (37, 768), (9, 1024),
+                                       (3, 1600), (6, 1796), (4, 2048), (3, 2052), (7, 4096),
                                        (16384, 768)])
 @pytest.mark.parametrize("xd,yd", [(F32, F32), (BF16, BF16), (F32, BF16)])
 def test_layer_norm(gpu, rows, cols, xd, yd):
@@ -74,8 +75,8 @@ def test_layer_norm(gpu, rows, cols, xd, yd):
 
 
 @pytest.mark.parametrize("dd", [F32, BF16])
-def test_add_layer_norm_writes_residual(gpu, dd):
-    rows, cols = 300, 768
+@pytest.mark.parametrize("rows,cols", [(300, 768), (301, 48), (33, 1600), (5, 4096)])
+def test_add_layer_norm_writes_residual(gpu, dd, rows, cols):
     x = randn(rows, cols, seed=3)
     d = randn(rows, cols, seed=4, dtype=dd)
     w, b = randn(cols, seed=5) + 1, randn(cols, seed=6)
