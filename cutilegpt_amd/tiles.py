@@ -25,6 +25,8 @@ Tile ids index the configuration table compiled into libcgpt.so
     bf16, the 2-stage 256x256 pipeline with each wave's output rows staged
     through its own LDS slot and stored as whole lines:
           15 = 256x256 (8 waves of 128x64)
+          16 = the same with non-temporal stores (outputs larger than the
+               256 MiB MALL, e.g. the LM head's fp32 logits)
     fp32: 0 = 128x128, 1 = 64x64
 
 ``TABLE`` maps exact (dtype, M, N, K) problems measured on MI355X to the tile
@@ -47,12 +49,12 @@ TABLE: Dict[Tuple[int, int, int, int], int] = {
     (_B, 16384, 768, 768): 14,    # attn c_proj  841
     (_B, 16384, 3072, 768): 15,   # c_fc         992 (867 with the GELU epilogue)
     (_B, 16384, 768, 3072): 14,   # mlp c_proj  1202
-    (_B, 16384, 50304, 768): 15,  # lm head (vocab padded), fp32 out 830
+    (_B, 16384, 50304, 768): 16,  # lm head (vocab padded), fp32 out 963
     # 'medium' (8L, d 512) prefill, M = 16 x 256
     (_B, 4096, 1536, 512): 14,    # 431
     (_B, 4096, 2048, 512): 14,    # 533
     (_B, 4096, 512, 2048): 3,     # 271
-    (_B, 4096, 50304, 512): 15,   # lm head (vocab padded), fp32 out 699
+    (_B, 4096, 50304, 512): 16,   # lm head (vocab padded), fp32 out
 }
 
 

@@ -132,7 +132,7 @@ def test_gemm_every_bf16_tile(gpu, tile, m, n, k):
     close(out, gemm_ref(a, w, b, _lib.EPI_BIAS), 1e-3, 2 ** -8, f"tile {tile}")
 
 
-DMA_TILES = [5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15]
+DMA_TILES = [5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16]
 
 
 @pytest.mark.parametrize("tile", DMA_TILES)
@@ -149,7 +149,7 @@ def test_gemm_dma_tiles(gpu, tile, m, n, k, epi):
     close(out, ref, 1e-4 * math.sqrt(k / 64), 1e-5, f"dma tile {tile} {m}x{n}x{k}")
 
 
-PERSIST_TILES = [5, 7, 9, 10, 11, 12, 13, 14, 15]
+PERSIST_TILES = [5, 7, 9, 10, 11, 12, 13, 14, 15, 16]
 
 
 @pytest.mark.parametrize("tile", PERSIST_TILES)
@@ -168,7 +168,7 @@ def test_gemm_persistent_tiles(gpu, tile, m, n, k, epi):
     close(out, ref, 2e-3, 2 ** -8, f"persistent tile {tile} {m}x{n}x{k}")
 
 
-@pytest.mark.parametrize("tile", [14, 15])
+@pytest.mark.parametrize("tile", [14, 15, 16])
 @pytest.mark.parametrize("ldc_pad,c_off,out_dtype", [(0, 0, BF16), (8, 0, BF16), (4, 4, BF16),
                                                       (0, 0, F32), (4, 0, F32), (0, 2, F32)])
 def test_gemm_staged_output_layouts(gpu, tile, ldc_pad, c_off, out_dtype):
