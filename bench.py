@@ -50,7 +50,7 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # Bytes beyond L2 per LM-head launch (2.0 x FETCH_SIZE + 1.0 x WRITE_SIZE, factors from
 # a 1 GiB copy), measured with rocprofv3 --pmc on the GPT-2 workload; see
 # profiles/lm_head_gemm_gpt2_traffic_pmc.md.  Only valid for the gpt2 workload.
-LM_HEAD_TRAFFIC_BYTES = 5.17e9
+LM_HEAD_TRAFFIC_BYTES = 5.05e9
 
 WORKLOADS = {
     "gpt2": dict(n_layer=12, n_head=12, n_embd=768, batch=16, seq=1024,
@@ -225,7 +225,7 @@ def main():
         "config": {"workload": wl["name"], "n_layer": L, "n_head": H, "n_embd": D,
                    "vocab_size": V, "batch": B, "seq_len": T, "logits": "fp32",
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "kernel": "lm_head GEMM (gemm_pipe_kernel 256x256, wave-staged whole-line stores, bf16 in, fp32 out, N=50257 padded to 50304, K=768)",
+        "roofline": {"bound": "mfma", "kernel": "lm_head GEMM (gemm_pipe_kernel 256x256, wave-staged whole-line non-temporal stores, bf16 in, fp32 out, N=50257 padded to 50304, K=768)",
                      "achieved": round(head_tflops, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(head_tflops / PEAK_BF16_TFLOPS, 4),
                      "traffic": LM_HEAD_TRAFFIC_BYTES if args.workload == "gpt2" else None,
