@@ -296,9 +296,11 @@ __device__ __forceinline__ void wait_stages(int later, bool stores) {
 constexpr uint32_t kBufferRsrcWord3 = 0x00020000u;  // raw buffer, gfx9 family
 
 // Output modes of gemm_pipe_kernel.  kOutWaveStagedNT is kOutWaveStaged with
-// non-temporal stores, for outputs larger than the MALL (the LM head's
-// logits): nothing would still be cached when a consumer reads them, and
-// streaming stores write them 20 % faster (1.58 -> 1.31 ms for the GPT-2 head).
+// non-temporal stores: the LM head's logits (larger than the MALL, so nothing
+// would still be cached for a consumer) are written 20 % faster (1.58 -> 1.31
+// ms for the GPT-2 head), and c_fc + GELU runs 10 % faster (858 -> 947
+// TFLOP/s in the GPT-2 forward) with the next GEMM reading its output no
+// slower.
 constexpr int kOutPlain = 0, kOutBuffer = 1, kOutWaveStaged = 2, kOutWaveStagedNT = 3;
 
 
@@ -887,6 +889,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_a3_kernel(
 // stage g its buffer can be refilled.  Output rows are staged through LDS and
 // stored as whole lines (requires 16-byte aligned rows and N a multiple of
 // 16 bytes' worth of elements).
+// Output stores are non-temporal: in the GPT-2 forward this took c_attn from
+// 826 to 900 TFLOP/s and attn c_proj from 741 to 783, the attention that reads
+// c_attn's output lost 7 %, and the forward gained 1.2 %.
+constexpr int kSlabStorePolicy = 2;
+
 template <int BM, int BN, int WGM, int WGN, int EPI, typename TOut>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_slab_kernel(
     const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, const void* __restrict__ bias,
@@ -1095,7 +1102,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_slab_kernel(
         const uint32_t off = ncol < N ? static_cast<uint32_t>(
                                             (static_cast<int64_t>(grow) * ldc + ncol) * sizeof(TOut))
                                       : 0x80000000u;
-        __builtin_amdgcn_raw_buffer_store_b128(d, rc, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(d, rc, off, 0, kSlabStorePolicy);
         __builtin_amdgcn_sched_barrier(0);
       }
       if (p + 1 < NPASS) {
@@ -1174,7 +1181,7 @@ static const TileCfg kBf16Tiles[] = {
     {256, 192, 2, 4},  // 13: 8 waves (128x48), A 3 buffers / W 2, 144 KiB
     {256, 192, 2, 4},  // 14: 8 waves (128x48), fragment reads one slab ahead, 112 KiB
     {256, 256, 2, 4},  // 15: 8 waves (128x64), SPS 2, 2 stages, rows staged per wave, 160 KiB
-    {256, 256, 2, 4},  // 16: 15 with non-temporal output stores (outputs larger than the MALL)
+    {256, 256, 2, 4},  // 16: 15 with non-temporal output stores
 };
 constexpr int kFirstPipeTile = 5;
 static const int kPipeSps[] = {2, 1, 2, 2, 2, 2, 1, 2, 2, 2, 2, 2};
@@ -1388,16 +1395,39 @@ static int launch_tile(int tile, const void* a, const void* w, const void* bias,
 // Default tile choice when the caller's table has no entry: the register-staged
 // kernel with the largest tile that still gives every CU about two blocks
 // (128x128 for long K, 128x64 otherwise), smaller tiles for small grids.
-static int auto_tile(bool bf16, int M, int N, int K, int64_t lda, int64_t ldw, int out_bytes) {
-  // Problems with at least one 256x192 tile per CU: the persistent
-  // direct-to-LDS pipelines (256x256 with wave-staged stores for wide N, as
-  // the LM heads measured best, non-temporal when the output exceeds the
-  // 256 MiB MALL; 256x192 with block-staged stores otherwise).
+static int auto_tile(bool bf16, int M, int N, int K, int64_t lda, int64_t ldw, int epi) {
+  // bf16 problems with at least one 256x192 tile per CU: the persistent
+  // direct-to-LDS pipelines — 256x256 with wave-staged non-temporal stores
+  // for wide N (the LM heads) and for the GELU epilogue; 256x192 with
+  // block-staged stores otherwise.  With fewer
+  // tiles than CUs, the persistent 256x192, 256x128 or 128x256 tile whose
+  // last round leaves the fewest CUs idle (ties to the larger tile), as long
+  // as it still gives half the CUs a tile; below that the register-staged
+  // kernel with smaller tiles.
   if (bf16) {
-    const int64_t tiles = static_cast<int64_t>((M + 255) / 256) * ((N + 191) / 192);
-    const bool streamed = static_cast<int64_t>(M) * N * out_bytes > (int64_t{256} << 20);
-    const int pick = N >= 16384 ? (streamed ? 16 : 15) : 14;
-    if (tiles >= 256 && pipe_ok(pick, M, N, K, lda, ldw)) return pick;
+    auto tiles = [&](int bm, int bn) {
+      return static_cast<int64_t>((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    };
+    const int cus = num_cus();
+    const int64_t t14 = tiles(256, 192);
+    if (t14 >= cus) {
+      const int pick = (N >= 16384 || epi == CGPT_EPI_BIAS_GELU) ? 16 : 14;
+      if (pipe_ok(pick, M, N, K, lda, ldw)) return pick;
+    } else {
+      const int64_t cand_t[3] = {t14, tiles(256, 128), tiles(128, 256)};
+      const int cand_id[3] = {14, 9, 10};
+      int best = -1;
+      double best_util = 0.0;
+      for (int i = 0; i < 3; ++i) {
+        const int64_t rounds = (cand_t[i] + cus - 1) / cus;
+        const double util = static_cast<double>(cand_t[i]) / static_cast<double>(rounds * cus);
+        if (cand_t[i] * 2 >= cus && util > best_util + 1e-9 && pipe_ok(cand_id[i], M, N, K, lda, ldw)) {
+          best = cand_id[i];
+          best_util = util;
+        }
+      }
+      if (best >= 0) return best;
+    }
   }
   const TileCfg* t = bf16 ? kBf16Tiles : kF32Tiles;
   const int nt = bf16 ? kNumBf16Tiles : kNumF32Tiles;
@@ -1530,7 +1560,7 @@ extern "C" int cgpt_gemm(const void* a, const void* w, const void* bias, void* c
   }
   if (tile == CGPT_TILE_AUTO)
     tile = auto_tile(bf16, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), lda, ldw,
-                     out_dtype == CGPT_F32 ? 4 : 2);
+                     epilogue);
   if (tile < 0 || tile >= nt) return CGPT_EINVAL;
   if (bf16 && tile >= kFirstPipeTile && !pipe_ok(tile, M, N, K, lda, ldw)) return CGPT_ESHAPE;
   const int64_t out_align = out_dtype == CGPT_F32 ? 16 : 8;

@@ -20,18 +20,20 @@ Tile ids index the configuration table compiled into libcgpt.so
           12 = 256x256                             13 = 256x192
     bf16, 2 stages of 2 slabs with each slab's fragment reads issued while the
     previous slab's MFMAs run, output rows staged through LDS and stored as
-    whole lines (rows of 16-byte multiples; otherwise the 2-stage kernel):
+    whole lines with non-temporal stores (rows of 16-byte multiples;
+    otherwise the 2-stage kernel):
           14 = 256x192 (8 waves of 128x48)
     bf16, the 2-stage 256x256 pipeline with each wave's output rows staged
     through its own LDS slot and stored as whole lines:
           15 = 256x256 (8 waves of 128x64)
-          16 = the same with non-temporal stores (outputs larger than the
-               256 MiB MALL, e.g. the LM head's fp32 logits)
+          16 = the same with non-temporal stores (the LM heads' fp32 logits,
+               c_fc + GELU)
     fp32: 0 = 128x128, 1 = 64x64
 
 ``TABLE`` maps exact (dtype, M, N, K) problems measured on MI355X to the tile
 that won; anything else falls back to the library's own heuristic
-(``TILE_AUTO``: the largest tile whose grid fills the 256 CUs).
+(``TILE_AUTO``: the persistent tile that fills the 256 CUs best, else the
+register-staged kernel's largest tile giving every CU about two blocks).
 """
 
 from __future__ import annotations
@@ -47,13 +49,13 @@ TABLE: Dict[Tuple[int, int, int, int], int] = {
     # GPT-2 124M prefill, M = 16 x 1024
     (_B, 16384, 2304, 768): 14,   # c_attn       981
     (_B, 16384, 768, 768): 14,    # attn c_proj  841
-    (_B, 16384, 3072, 768): 15,   # c_fc         992 (867 with the GELU epilogue)
+    (_B, 16384, 3072, 768): 16,   # c_fc + GELU   947 in the forward (858 on id 15)
     (_B, 16384, 768, 3072): 14,   # mlp c_proj  1202
     (_B, 16384, 50304, 768): 16,  # lm head (vocab padded), fp32 out 963
     # 'medium' (8L, d 512) prefill, M = 16 x 256
     (_B, 4096, 1536, 512): 14,    # 431
-    (_B, 4096, 2048, 512): 14,    # 533
-    (_B, 4096, 512, 2048): 3,     # 271
+    (_B, 4096, 2048, 512): 10,    # 520 (GELU epilogue)
+    (_B, 4096, 512, 2048): 4,     # 361
     (_B, 4096, 50304, 512): 16,   # lm head (vocab padded), fp32 out
 }
 
