@@ -180,10 +180,10 @@ def main():
         "gemm_mlp_proj": ("TFLOP/s", L * 2 * M * 4 * D * D),
         "lm_head": ("TFLOP/s", head_f),
         "attention": ("TFLOP/s", attn_f),
-        # add+LN: read x fp32 + delta bf16, write x fp32 + y bf16 (first: read x, write y)
-        "ln": ("GB/s", (2 * L) * M * D * (4 + 2 + 4 + 2) + M * D * (4 + 2)),
-        # gather: read wte + wpe rows bf16, write x fp32
-        "embedding": ("GB/s", M * D * (2 + 2 + 4)),
+        # add+LN: read x fp32 + delta bf16, write x fp32 + y bf16 (the last: no x write)
+        "ln": ("GB/s", (2 * L - 1) * M * D * (4 + 2 + 4 + 2) + M * D * (4 + 2 + 2)),
+        # gather + layer 0's LN: read wte + wpe rows bf16, write x fp32 + y bf16
+        "embedding": ("GB/s", M * D * (2 + 2 + 4 + 2)),
     }
     breakdown = {}
     for tag, (ms, n) in per.items():

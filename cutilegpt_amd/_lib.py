@@ -49,6 +49,8 @@ SIGNATURES = {
                                 _I64, _I64, _I64, _F, _I, _I, _P]),
     "cgpt_embedding": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _P, _P]),
     "cgpt_embedding_at": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _I, _I, _P, _P]),
+    "cgpt_embedding_layernorm": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
+                                      _I64, _I64, _F, _I, _I, _P, _P]),
     "cgpt_attention_decode": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P,
                                    _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
                                    _I64, _I64, _F, _I, _P, _P]),

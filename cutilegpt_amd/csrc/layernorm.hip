@@ -217,6 +217,119 @@ static int launch_ln3(const void* x, const void* delta, void* x_out, const void*
   return hip_status(hipGetLastError());
 }
 
+// ---- token + position embedding fused with the first LayerNorm
+//
+// One wave per token, as add_layernorm_kernel without a delta: the gathered
+// row x = wte[id] + wpe[pos] (fp32, the residual stream) is written once and
+// normalised from registers, so the LayerNorm does not read it back.  The
+// arithmetic (fp32 sum of the two rows, two-pass mean / centred variance,
+// the same reduction order) equals the embedding kernel followed by
+// add_layernorm_kernel bit for bit.  Ids / positions out of range are clamped
+// and flagged as in the embedding kernel.
+template <typename TW, typename TY, int NCH>
+__global__ __launch_bounds__(kLnThreads) void embedding_layernorm_kernel(
+    const int64_t* __restrict__ idx, const TW* __restrict__ wte, const TW* __restrict__ wpe,
+    const int* __restrict__ pos_dev, float* __restrict__ x_out, const void* __restrict__ gamma,
+    const void* __restrict__ beta, TY* __restrict__ y, int64_t n_tokens, int64_t T, int cols,
+    int64_t vocab, int64_t pos0, int64_t n_pos, float eps, int* err_flag) {
+  const int lane = threadIdx.x & 63;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kLnRowsPerBlock + (threadIdx.x >> 6);
+  if (i >= n_tokens) return;
+  int64_t id = idx[i];
+  bool bad = false;
+  if (id < 0 || id >= vocab) {
+    bad = true;
+    id = id < 0 ? 0 : vocab - 1;
+  }
+  int64_t pos = pos0 + (pos_dev != nullptr ? static_cast<int64_t>(*pos_dev) : i % T);
+  if (pos < 0 || pos >= n_pos) {
+    bad = true;
+    pos = pos < 0 ? 0 : n_pos - 1;
+  }
+  if (bad && err_flag != nullptr && lane == 0) *err_flag = 1;
+  constexpr bool kParamBf16 = sizeof(TW) == 2;
+  const int pshift = kParamBf16 ? 1 : 2;
+  const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(gamma), 0, cols << pshift, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(beta), 0, cols << pshift, 0x00020000);
+  const TW* trow = wte + id * cols;
+  const TW* prow = wpe + pos * cols;
+  float v[NCH][4], pv[NCH][4];
+  u32x4_t graw[NCH], braw[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int col = (c * 64 + lane) * 4;
+    const int cc = col < cols ? col : 0;
+    load4(trow + cc, v[c]);
+    load4(prow + cc, pv[c]);
+    graw[c] = __builtin_amdgcn_raw_buffer_load_b128(rg, cc << pshift, 0, 0);
+    braw[c] = __builtin_amdgcn_raw_buffer_load_b128(rb, cc << pshift, 0, 0);
+  }
+  const float n_f = static_cast<float>(cols);
+  float sum = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const bool ok = (c * 64 + lane) * 4 < cols;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float t = v[c][j] + pv[c][j];
+      v[c][j] = ok ? t : 0.f;
+      sum += v[c][j];
+    }
+  }
+  const float mean = wave_sum(sum) / n_f;
+  float sq = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const bool ok = (c * 64 + lane) * 4 < cols;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float t = v[c][j] - mean;
+      sq += ok ? t * t : 0.f;
+    }
+  }
+  const float rstd = 1.0f / sqrtf(wave_sum(sq) / n_f + eps);
+  const int64_t base = i * cols;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int col = (c * 64 + lane) * 4;
+    if (col < cols) {
+      float gm[4], bt[4];
+      decode_param(graw[c], kParamBf16, gm);
+      decode_param(braw[c], kParamBf16, bt);
+      store4(x_out + base + col, v[c]);
+      float o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = (v[c][j] - mean) * rstd * gm[j] + bt[j];
+      store4(y + base + col, o);
+    }
+  }
+}
+
+template <typename TW, typename TY>
+static int launch_emb_ln(const int64_t* idx, const void* wte, const void* wpe, const int* pos_dev,
+                         float* x_out, const void* gamma, const void* beta, void* y,
+                         int64_t n_tokens, int64_t T, int cols, int64_t vocab, int64_t pos0,
+                         int64_t n_pos, float eps, int* err, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((n_tokens + kLnRowsPerBlock - 1) / kLnRowsPerBlock));
+  const TW* tw = static_cast<const TW*>(wte);
+  const TW* pw = static_cast<const TW*>(wpe);
+  TY* yp = static_cast<TY*>(y);
+#define CGPT_EMB_LN(NCH)                                                                        \
+  hipLaunchKernelGGL((embedding_layernorm_kernel<TW, TY, NCH>), grid, dim3(kLnThreads), 0, s, idx, \
+                     tw, pw, pos_dev, x_out, gamma, beta, yp, n_tokens, T, cols, vocab, pos0,   \
+                     n_pos, eps, err)
+  if (cols <= 512) CGPT_EMB_LN(2);
+  else if (cols <= 768) CGPT_EMB_LN(3);
+  else if (cols <= 1024) CGPT_EMB_LN(4);
+  else if (cols <= 1792) CGPT_EMB_LN(7);
+  else if (cols <= 2048) CGPT_EMB_LN(8);
+  else CGPT_EMB_LN(16);
+#undef CGPT_EMB_LN
+  return hip_status(hipGetLastError());
+}
+
 template <typename TX, typename TD>
 static int launch_ln2(int y_dtype, const void* x, const void* delta, void* x_out,
                       const void* gamma, const void* beta, bool param_bf16, void* y,
@@ -450,4 +563,34 @@ extern "C" int cgpt_add_layernorm_partials(const void* x, const float* partials,
   return y_dtype == CGPT_BF16
              ? launch_lnp<float, bf16_t>(xp, partials, n, ps, lp, bias, xo, gamma, beta, pb, y, r, c, eps, s)
              : launch_lnp<float, float>(xp, partials, n, ps, lp, bias, xo, gamma, beta, pb, y, r, c, eps, s);
+}
+
+extern "C" int cgpt_embedding_layernorm(const int64_t* idx, const void* wte, const void* wpe,
+                                        const int* pos_dev, float* x_out, const void* gamma,
+                                        const void* beta, void* y, int64_t n_tokens, int64_t T,
+                                        int64_t D, int64_t vocab, int64_t pos0, int64_t n_pos,
+                                        float eps, int w_dtype, int y_dtype, int* err_flag,
+                                        void* stream) {
+  using namespace cgpt;
+  if (n_tokens < 0 || D <= 0 || vocab <= 0 || n_pos <= 0) return CGPT_EINVAL;
+  if (n_tokens == 0) return CGPT_OK;
+  if (idx == nullptr || wte == nullptr || wpe == nullptr || x_out == nullptr || gamma == nullptr ||
+      beta == nullptr || y == nullptr || T <= 0)
+    return CGPT_EINVAL;
+  if (!dtype_ok(w_dtype) || !dtype_ok(y_dtype)) return CGPT_EDTYPE;
+  if (D % 4 != 0 || D > 4096) return CGPT_ESHAPE;
+  if (!ptr_aligned(wte, w_dtype) || !ptr_aligned(wpe, w_dtype) || !ptr_aligned(gamma, w_dtype) ||
+      !ptr_aligned(beta, w_dtype) || !aligned16(x_out) || !ptr_aligned(y, y_dtype) ||
+      (reinterpret_cast<uintptr_t>(idx) & 7))
+    return CGPT_EINVAL;
+  if (!(eps >= 0.f)) return CGPT_EINVAL;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int c = static_cast<int>(D);
+  if (w_dtype == CGPT_BF16)
+    return y_dtype == CGPT_BF16
+               ? launch_emb_ln<bf16_t, bf16_t>(idx, wte, wpe, pos_dev, x_out, gamma, beta, y, n_tokens, T, c, vocab, pos0, n_pos, eps, err_flag, s)
+               : launch_emb_ln<bf16_t, float>(idx, wte, wpe, pos_dev, x_out, gamma, beta, y, n_tokens, T, c, vocab, pos0, n_pos, eps, err_flag, s);
+  return y_dtype == CGPT_BF16
+             ? launch_emb_ln<float, bf16_t>(idx, wte, wpe, pos_dev, x_out, gamma, beta, y, n_tokens, T, c, vocab, pos0, n_pos, eps, err_flag, s)
+             : launch_emb_ln<float, float>(idx, wte, wpe, pos_dev, x_out, gamma, beta, y, n_tokens, T, c, vocab, pos0, n_pos, eps, err_flag, s);
 }

@@ -5,8 +5,8 @@ whole forward on the growing prefix for every new token.  Here a prompt is run
 once (prefill) while its keys and values are stored into a per-layer cache,
 and every further token costs one step over B rows:
 
-    embedding at position pos        cgpt_embedding_at (pos read on device)
-    LN_1 of layer 0                  cgpt_add_layernorm
+    embedding at position pos        cgpt_embedding_layernorm (pos read on
+      + LN_1 of layer 0                device, one pass)
     per layer: QKV GEMM              cgpt_gemm_partials (split-K partial products)
                attention             cgpt_attention_decode_partials (adds the
                                      partials + bias, appends k, v at pos)
@@ -178,10 +178,12 @@ class DecodeSession:
                                                 W[wk + ".bias"].data_ptr(), ph, B, D, 1e-5, f32,
                                                 ac, ac, ac, s), "add_layernorm_partials")
 
-        chk(lib.cgpt_embedding_at(self.ids.data_ptr(), W["wte"].data_ptr(), W["wpe"].data_ptr(),
-                                  px, B, D, V, self.t0, pstep, cfg.block_size, ac, f32,
-                                  self.err.data_ptr(), s), "embedding_at")
-        add_ln(None, "h.0.ln_1")
+        chk(lib.cgpt_embedding_layernorm(self.ids.data_ptr(), W["wte"].data_ptr(),
+                                         W["wpe"].data_ptr(), pstep, px,
+                                         W["h.0.ln_1.weight"].data_ptr(),
+                                         W["h.0.ln_1.bias"].data_ptr(), ph, B, 1, D, V, self.t0,
+                                         cfg.block_size, 1e-5, ac, ac, self.err.data_ptr(), s),
+            "embedding_layernorm")
         csb, csh, cst = self.cache.strides()
         t_max = self.cache.t_max
         scale = 1.0 / math.sqrt(hd)

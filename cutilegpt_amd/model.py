@@ -7,8 +7,8 @@ Same surface as ``cutile_gpt/models/gpt.py:24-343``: ``CutileGPT(config)``, the
 
 Forward data flow on one GPU (M = B*T rows, D = n_embd):
 
-    x  (M, D)  fp32 residual stream           <- embedding gather + position add
-    h  (M, D)  act dtype  = LN(x)              <- fused add + LayerNorm kernel
+    x  (M, D)  fp32 residual stream           <- embedding gather + position add,
+    h  (M, D)  act dtype  = LN1(x)                fused with layer 0's LayerNorm
     qkv(M, 3D) act dtype  = h Wqkv^T + b       <- MFMA GEMM, bias epilogue
     a  (M, D)  act dtype  = attention(qkv)     <- flash attention reading qkv strided
     d  (M, D)  act dtype  = a Wo^T + b         <- GEMM
@@ -218,12 +218,14 @@ class CutileGPT:
                                        ph, M, D, 1e-5, f32, ac, ac, ac, s), "add_layernorm")
             mark("ln", False)
 
+        # x = wte[idx] + wpe[pos] and h = ln_1(x) of layer 0 in one pass.
         mark("embedding", True)
-        chk(lib.cgpt_embedding(idx.data_ptr(), W["wte"].data_ptr(), W["wpe"].data_ptr(), px, M, T,
-                               D, V, 0, cfg.block_size, ac, f32, self._err.data_ptr(), s),
-            "embedding")
+        chk(lib.cgpt_embedding_layernorm(idx.data_ptr(), W["wte"].data_ptr(), W["wpe"].data_ptr(),
+                                         None, px, W["h.0.ln_1.weight"].data_ptr(),
+                                         W["h.0.ln_1.bias"].data_ptr(), ph, M, T, D, V, 0,
+                                         cfg.block_size, 1e-5, ac, ac, self._err.data_ptr(), s),
+            "embedding_layernorm")
         mark("embedding", False)
-        add_ln(None, "h.0.ln_1")
         st_qkv = (T * 3 * D, hd, 3 * D)
         st_o = (T * D, hd, D)
         scale = 1.0 / math.sqrt(hd)

@@ -211,6 +211,25 @@ int cgpt_embedding_at(const int64_t* idx, const void* wte, const void* wpe, void
                       int* err_flag, void* stream);
 
 /*
+ * Token + position embedding fused with the first LayerNorm (ln_1 of layer 0):
+ *   x_out[i, :] = wte[idx[i], :] + wpe[pos_i, :]                 (fp32 residual stream)
+ *   y[i, :]     = (x_out[i, :] - mean) / sqrt(var + eps) * gamma + beta
+ * with pos_i = pos0 + i % T, or pos0 + *pos_dev for every token when pos_dev is
+ * not NULL (a decode step; T is then ignored).  wte, wpe, gamma and beta are
+ * w_dtype, y is y_dtype; D % 4 == 0, D <= 4096.  Clamping and err_flag as
+ * cgpt_embedding.  x_out and y equal, bit for bit, cgpt_embedding into an
+ * fp32 buffer followed by cgpt_add_layernorm on it without a delta — one HBM
+ * pass fewer (the LayerNorm does not read the rows back).
+ * Replaces the embedding and the first LayerNorm of CutileGPT.forward,
+ * cutile_gpt/models/gpt.py:110-113 and :120-122 (layer 0).
+ */
+int cgpt_embedding_layernorm(const int64_t* idx, const void* wte, const void* wpe,
+                             const int* pos_dev, float* x_out, const void* gamma,
+                             const void* beta, void* y, int64_t n_tokens, int64_t T, int64_t D,
+                             int64_t vocab, int64_t pos0, int64_t n_pos, float eps, int w_dtype,
+                             int y_dtype, int* err_flag, void* stream);
+
+/*
  * Single-query attention over a KV cache, one decode step for B sequences x H
  * heads.  Cache element (b, h, t, d) lives at base + b*c_sb + h*c_sh + t*c_st + d
  * (k_cache and v_cache share the strides; 16-byte aligned rows).  With

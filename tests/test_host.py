@@ -68,6 +68,13 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert lib.cgpt_gelu(fake, fake, 10, 9, None) == -2
     assert lib.cgpt_gelu(None, None, 0, 0, None) == 0
     assert lib.cgpt_embedding(fake, fake, None, fake, 4, 4, 6, 10, 0, 0, 0, 0, None, None) == -3
+    # embedding + LayerNorm: D not a multiple of 4, missing wpe, bad dtype, misaligned x_out
+    el = lambda wpe, x, D, wd: lib.cgpt_embedding_layernorm(fake, fake, wpe, None, x, fake, fake, fake,
+                                                             4, 4, D, 10, 0, 8, 1e-5, wd, 0, None, None)
+    assert el(fake, fake, 6, 0) == -3
+    assert el(None, fake, 8, 0) == -1
+    assert el(fake, fake, 8, 4) == -2
+    assert el(fake, fake + 4, 8, 0) == -1
 
 
 def test_wrappers_reject_host_tensors():

@@ -320,3 +320,59 @@ def test_embedding_gather_and_range_check(gpu):
     assert torch.equal(out, w[idx])
     with pytest.raises(IndexError):  # clamped in the kernel, reported on the host
         cg.cutile_embedding(torch.tensor([3, 100]).to(gpu), w.to(gpu))
+
+
+@pytest.mark.parametrize("wd,yd", [(F32, F32), (BF16, BF16), (BF16, F32)])
+@pytest.mark.parametrize("D", [48, 768, 1600, 2052])
+def test_embedding_layernorm_equals_embedding_then_ln(gpu, wd, yd, D):
+    """cgpt_embedding_layernorm == cgpt_embedding (fp32 out) then LayerNorm, bit for bit,
+    and within LayerNorm tolerance of the fp64 oracle."""
+    V, P, B, T = 1000, 64, 3, 21
+    wte, wpe = randn(V, D, seed=11, dtype=wd), randn(P, D, seed=12, dtype=wd)
+    g = (1 + randn(D, seed=13, scale=0.1)).to(wd)
+    b = randn(D, seed=14, scale=0.1).to(wd)
+    idx = torch.randint(0, V, (B, T), generator=torch.Generator().manual_seed(15))
+    dg = [t.to(gpu) for t in (wte, wpe, g, b, idx)]
+    x2 = cg.token_pos_embedding(dg[4], dg[0], dg[1], pos0=7, out_dtype=F32)
+    y2 = cg.add_layer_norm(x2, None, dg[2], dg[3], out_dtype=yd)
+    x1 = torch.empty(B * T, D, device=gpu)
+    y1 = torch.empty(B * T, D, dtype=yd, device=gpu)
+    err = torch.zeros(1, dtype=torch.int32, device=gpu)
+    lib = _lib.load()
+    code = {F32: _lib.CGPT_F32, BF16: _lib.CGPT_BF16}
+    _lib.check(lib.cgpt_embedding_layernorm(
+        dg[4].data_ptr(), dg[0].data_ptr(), dg[1].data_ptr(), None, x1.data_ptr(), dg[2].data_ptr(),
+        dg[3].data_ptr(), y1.data_ptr(), B * T, T, D, V, 7, P, 1e-5, code[wd], code[yd],
+        err.data_ptr(), torch.cuda.current_stream().cuda_stream), "embedding_layernorm")
+    torch.cuda.synchronize()
+    assert err.item() == 0
+    assert torch.equal(x1.view(B, T, D), x2.view(B, T, D))
+    assert torch.equal(y1.view(B, T, D), y2.view(B, T, D))
+    xr = wte.double()[idx] + wpe.double()[7:7 + T].unsqueeze(0)
+    ref = R.layer_norm(xr, g.double(), b.double())
+    close(y1.view(B, T, D), ref, 1e-5, 1e-5 if yd == F32 else 2 ** -8 + 1e-5, "emb+ln")
+
+
+def test_embedding_layernorm_device_position_and_clamp(gpu):
+    """Decode form: the position comes from device memory; out-of-range ids are
+    clamped and flagged."""
+    V, P, D = 97, 32, 64
+    wte, wpe = randn(V, D, seed=21, dtype=BF16).to(gpu), randn(P, D, seed=22, dtype=BF16).to(gpu)
+    g = torch.ones(D, dtype=BF16, device=gpu)
+    b = torch.zeros(D, dtype=BF16, device=gpu)
+    idx = torch.tensor([3, 96, 0, 500], dtype=torch.int64, device=gpu)
+    pdev = torch.tensor([6], dtype=torch.int32, device=gpu)
+    x = torch.empty(4, D, device=gpu)
+    y = torch.empty(4, D, dtype=BF16, device=gpu)
+    err = torch.zeros(1, dtype=torch.int32, device=gpu)
+    lib = _lib.load()
+    _lib.check(lib.cgpt_embedding_layernorm(
+        idx.data_ptr(), wte.data_ptr(), wpe.data_ptr(), pdev.data_ptr(), x.data_ptr(), g.data_ptr(),
+        b.data_ptr(), y.data_ptr(), 4, 1, D, V, 10, P, 1e-5, _lib.CGPT_BF16, _lib.CGPT_BF16,
+        err.data_ptr(), torch.cuda.current_stream().cuda_stream), "embedding_layernorm")
+    torch.cuda.synchronize()
+    ids = torch.tensor([3, 96, 0, V - 1], device=gpu)
+    assert torch.equal(x, wte[ids].float() + wpe[16].float())
+    assert err.item() == 1
+    close(y, R.layer_norm(x.double().cpu(), g.double().cpu(), b.double().cpu()), 1e-5,
+          2 ** -8 + 1e-5, "emb+ln decode")
