@@ -91,16 +91,22 @@ def save_hf_checkpoint(path: str, weights: Dict[str, torch.Tensor], config: GPTC
               metadata={"format": "pt"})
 
 
-def load_hf_checkpoint(path: str) -> Tuple[Dict[str, torch.Tensor], GPTConfig]:
-    """Read an HF GPT-2 directory into (internal weight dict on CPU, GPTConfig)."""
+def load_hf_checkpoint(path: str, device: str = "cpu") -> Tuple[Dict[str, torch.Tensor], GPTConfig]:
+    """Read an HF GPT-2 directory into (internal weight dict, GPTConfig).
+
+    Tensors keep the checkpoint's dtype (a bf16 checkpoint is never widened on
+    the host) and are read straight onto ``device``: safetensors files are
+    loaded there by safetensors itself, ``pytorch_model.bin`` through
+    ``torch.load(map_location=device, weights_only=True)``.  The Conv1D
+    transposes are views; the model makes them contiguous on its device."""
     with open(os.path.join(path, "config.json")) as f:
         config = config_from_hf(json.load(f))
     st = os.path.join(path, "model.safetensors")
     if os.path.exists(st):
         from safetensors.torch import load_file
-        sd = load_file(st)
+        sd = load_file(st, device=str(device))
     else:
-        sd = torch.load(os.path.join(path, "pytorch_model.bin"), map_location="cpu",
+        sd = torch.load(os.path.join(path, "pytorch_model.bin"), map_location=str(device),
                         weights_only=True)
     return hf_to_internal(sd, config.n_layer), config
 
@@ -146,10 +152,11 @@ class HFWeightLoader:
         return self._tokenizer
 
 
-def resolve_checkpoint(name_or_path: str, n_layer: Optional[int] = None):
-    """Internal weight dict (CPU) + GPTConfig for a local dir or a cached HF name."""
+def resolve_checkpoint(name_or_path: str, n_layer: Optional[int] = None, device: str = "cpu"):
+    """Internal weight dict + GPTConfig for a local dir (read onto ``device``) or
+    a cached HF name (CPU)."""
     if os.path.isdir(name_or_path):
-        return load_hf_checkpoint(name_or_path)
+        return load_hf_checkpoint(name_or_path, device)
     from transformers import GPT2LMHeadModel
     model = GPT2LMHeadModel.from_pretrained(name_or_path)
     c = model.config

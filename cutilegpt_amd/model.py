@@ -345,7 +345,7 @@ class CutileGPT:
         Mirrors ``cutile_gpt/models/gpt.py:231-304`` (Conv1D transposed, tied head)."""
         from .hf_loader import resolve_checkpoint
 
-        w, config = resolve_checkpoint(model_name)
+        w, config = resolve_checkpoint(model_name, device=str(self.device))
         for f in ("n_layer", "n_head", "n_embd", "vocab_size"):
             if getattr(config, f) != getattr(self.config, f):
                 raise ValueError(f"checkpoint {f}={getattr(config, f)} does not match "
@@ -376,7 +376,7 @@ class CutileGPT:
         """Build a model sized from an HF directory's config.json and load it."""
         from .hf_loader import resolve_checkpoint
 
-        w, config = resolve_checkpoint(path)
+        w, config = resolve_checkpoint(path, device=device)
         model = cls.__new__(cls)
         model.config = config
         model.dtype = dtype
