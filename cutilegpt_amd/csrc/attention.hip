@@ -2,7 +2,8 @@
 //
 // Work decomposition
 //  * One block = 4 wavefronts = BQ = 128 queries of one (batch, head); each wave
-//    owns QT = 2 sub-tiles of 16 queries.  Blocks are ordered so that the last
+//    owns QT = 2 sub-tiles of 16 queries (the bf16 DMA kernel also has a
+//    64-query form, one sub-tile a wave, for small grids).  Blocks are ordered so that the last
 //    (most expensive, under the causal mask) query blocks are dispatched first.
 //  * Keys/values stream through LDS in BKV = 64-row blocks, double-buffered
 //    through registers (the loads of block j+1 are in flight while block j is
@@ -360,14 +361,14 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
 //    of the P operand (keys 32c + 4g + r, then 32c + 16 + 4g + r).
 //  * 16-byte chunk c of row r is stored at chunk c ^ (r & 7): the DMA lane
 //    that fills a slot fetches the chunk that belongs there.
-template <int HD, int STAGES>
+template <int HD, int STAGES, int QTW>
 __global__ __launch_bounds__(kAttnThreads) void attn_fwd_dma_kernel(
     const bf16_t* __restrict__ Q, const bf16_t* __restrict__ K, const bf16_t* __restrict__ V,
     bf16_t* __restrict__ O, int H, int Tq, int Tk, int64_t q_sb, int64_t q_sh, int64_t q_st,
     int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st,
     int64_t o_sb, int64_t o_sh, int64_t o_st, float scale_log2, int causal, int n_bh) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  constexpr int QT = kAttnQT, BQ = kAttnBQ, BKV = kAttnBKV;
+  constexpr int QT = QTW, BQ = 4 * 16 * QTW, BKV = kAttnBKV;
   constexpr int NWAVE = kAttnThreads / 64;
   constexpr int KROW = HD * 2;                 // bytes per K / V row
   constexpr int CPR = KROW / 16;               // 16-byte chunks per row
@@ -603,21 +604,46 @@ static bool attn_dma_ok(int Tk, const int64_t* st) {
          (static_cast<int64_t>(Tk) + 1) * st[8] * 2 < (int64_t{1} << 31);
 }
 
-template <int HD, int STAGES>
-static int launch_attn_dma(const void* q, const void* k, const void* v, void* o, int B, int H,
-                           int Tq, int Tk, const int64_t* st, float scale, int causal,
-                           hipStream_t s) {
+// Queries per block: 128 (2 sub-tiles of 16 a wave), or 64 (1 a wave) when
+// 128-query blocks would give fewer than four blocks per CU — small batches or
+// short sequences, where the launch is bound by its longest block.  Measured
+// (bit-identical outputs): 8x12x512 216 -> 263 TFLOP/s, 16x8x256 126 -> 154,
+// GPT-2 XL prefill 32x25x128 107 -> 118; at 16x12x1024 (6 blocks per CU) 64
+// queries fell from 542 to 454.
+template <int HD, int STAGES, int QTW>
+static int launch_attn_dma_qt(const void* q, const void* k, const void* v, void* o, int B, int H,
+                              int Tq, int Tk, const int64_t* st, float scale, int causal,
+                              hipStream_t s) {
+  constexpr int BQ = 4 * 16 * QTW;
   const int n_bh = B * H;
-  const int n_qblk = (Tq + kAttnBQ - 1) / kAttnBQ;
+  const int n_qblk = (Tq + BQ - 1) / BQ;
   const int64_t blocks = static_cast<int64_t>(n_bh) * n_qblk;
   if (blocks > 0x7fffffff) return CGPT_ESHAPE;
   const float scale_log2 = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL((attn_fwd_dma_kernel<HD, STAGES>), dim3(static_cast<unsigned>(blocks)),
+  hipLaunchKernelGGL((attn_fwd_dma_kernel<HD, STAGES, QTW>), dim3(static_cast<unsigned>(blocks)),
                      dim3(kAttnThreads), 0, s, static_cast<const bf16_t*>(q),
                      static_cast<const bf16_t*>(k), static_cast<const bf16_t*>(v),
                      static_cast<bf16_t*>(o), H, Tq, Tk, st[0], st[1], st[2], st[3], st[4], st[5],
                      st[6], st[7], st[8], st[9], st[10], st[11], scale_log2, causal, n_bh);
   return hip_status(hipGetLastError());
+}
+
+static int attn_num_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    return 256;
+  return n;
+}
+
+template <int HD, int STAGES>
+static int launch_attn_dma(const void* q, const void* k, const void* v, void* o, int B, int H,
+                           int Tq, int Tk, const int64_t* st, float scale, int causal,
+                           hipStream_t s) {
+  const int64_t blocks128 = static_cast<int64_t>(B) * H * ((Tq + 127) / 128);
+  if (blocks128 < 4 * static_cast<int64_t>(attn_num_cus()))
+    return launch_attn_dma_qt<HD, STAGES, 1>(q, k, v, o, B, H, Tq, Tk, st, scale, causal, s);
+  return launch_attn_dma_qt<HD, STAGES, 2>(q, k, v, o, B, H, Tq, Tk, st, scale, causal, s);
 }
 
 template <typename T, int HD>
