@@ -2,8 +2,8 @@
 //
 // Work decomposition
 //  * One block = 4 wavefronts = BQ = 128 queries of one (batch, head); each wave
-//    owns QT = 2 sub-tiles of 16 queries (the bf16 DMA kernel also has a
-//    64-query form, one sub-tile a wave, for small grids).  Blocks are ordered so that the last
+//    owns QT = 2 sub-tiles of 16 queries (both kernels also have a 64-query
+//    form, one sub-tile a wave, for small grids).  Blocks are ordered so that the last
 //    (most expensive, under the causal mask) query blocks are dispatched first.
 //  * Keys/values stream through LDS in BKV = 64-row blocks, double-buffered
 //    through registers (the loads of block j+1 are in flight while block j is
@@ -32,8 +32,6 @@
 namespace cgpt {
 
 constexpr int kAttnThreads = 256;
-constexpr int kAttnQT = 2;                         // 16-query sub-tiles per wave
-constexpr int kAttnBQ = 4 * 16 * kAttnQT;          // queries per block
 constexpr int kAttnBKV = 64;                       // keys per LDS block
 
 template <typename T> struct AttnMfma;
@@ -58,13 +56,13 @@ __device__ __forceinline__ void store4_o(bf16_t* p, const float* v) {
   *reinterpret_cast<u32x2_t*>(p) = u;
 }
 
-template <typename T, int HD>
+template <typename T, int HD, int QTW>
 __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V, T* __restrict__ O,
     int H, int Tq, int Tk, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh,
     int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t o_sb, int64_t o_sh,
     int64_t o_st, float scale_log2, int causal, int n_bh) {
-  constexpr int QT = kAttnQT, BQ = kAttnBQ, BKV = kAttnBKV;
+  constexpr int QT = QTW, BQ = 4 * 16 * QTW, BKV = kAttnBKV;
   constexpr int EPC = 16 / sizeof(T);          // elements per 16-byte chunk
   constexpr int CPR = HD / EPC;                // 16-byte chunks per K row
   constexpr int SWZ = (CPR < 8 ? CPR : 8) - 1; // chunk swizzle mask
@@ -653,16 +651,27 @@ static int launch_attn(const void* q, const void* k, const void* v, void* o, int
     if (attn_dma_ok(Tk, st))
       return launch_attn_dma<HD, HD == 64 ? 3 : 2>(q, k, v, o, B, H, Tq, Tk, st, scale, causal, s);
   }
+  // 64-query blocks when 128-query ones would give fewer than four per CU, as
+  // for the DMA kernel.
+  const int64_t blocks128 = static_cast<int64_t>(B) * H * ((Tq + 127) / 128);
+  const bool small = blocks128 < 4 * static_cast<int64_t>(attn_num_cus());
+  const int bq = small ? 64 : 128;
   const int n_bh = B * H;
-  const int n_qblk = (Tq + kAttnBQ - 1) / kAttnBQ;
+  const int n_qblk = (Tq + bq - 1) / bq;
   const int64_t blocks = static_cast<int64_t>(n_bh) * n_qblk;
   if (blocks > 0x7fffffff) return CGPT_ESHAPE;
   const float scale_log2 = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL((attn_fwd_kernel<T, HD>), dim3(static_cast<unsigned>(blocks)),
-                     dim3(kAttnThreads), 0, s, static_cast<const T*>(q), static_cast<const T*>(k),
-                     static_cast<const T*>(v), static_cast<T*>(o), H, Tq, Tk, st[0], st[1], st[2],
-                     st[3], st[4], st[5], st[6], st[7], st[8], st[9], st[10], st[11], scale_log2,
-                     causal, n_bh);
+#define CGPT_ATTN_LAUNCH(QTW)                                                                     \
+  hipLaunchKernelGGL((attn_fwd_kernel<T, HD, QTW>), dim3(static_cast<unsigned>(blocks)),            \
+                     dim3(kAttnThreads), 0, s, static_cast<const T*>(q), static_cast<const T*>(k), \
+                     static_cast<const T*>(v), static_cast<T*>(o), H, Tq, Tk, st[0], st[1], st[2], \
+                     st[3], st[4], st[5], st[6], st[7], st[8], st[9], st[10], st[11], scale_log2, \
+                     causal, n_bh)
+  if (small)
+    CGPT_ATTN_LAUNCH(1);
+  else
+    CGPT_ATTN_LAUNCH(2);
+#undef CGPT_ATTN_LAUNCH
   return hip_status(hipGetLastError());
 }
 
