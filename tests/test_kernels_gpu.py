@@ -122,6 +122,26 @@ def test_gemm_auto_tile(gpu, m, n, k, dtype, epi):
     close(out, ref, 1e-4 * math.sqrt(k / 64), 1e-5, f"gemm {dtype} {m}x{n}x{k} epi{epi}")
 
 
+@pytest.mark.parametrize("m,n,k,epi", [(4096, 1600, 1600, _lib.EPI_BIAS),    # XL prefill proj
+                                        (4096, 1600, 6400, _lib.EPI_BIAS),    # XL MLP proj
+                                        (4096, 6400, 1600, _lib.EPI_BIAS_GELU),
+                                        (2048, 3072, 768, _lib.EPI_BIAS_GELU)])
+def test_gemm_auto_tile_persistent_paths(gpu, m, n, k, epi):
+    """TILE_AUTO on shapes that take the persistent tiles chosen by the number of
+    idle CUs (fewer 256x192 tiles than CUs) or id 16 (GELU epilogue): equal, bit
+    for bit, to tile 15 (every bf16 kernel adds the same k32 MFMA products in
+    the same order), and close to the fp64 product."""
+    a = randn(m, k, seed=m + 1, dtype=BF16)
+    w = randn(n, k, seed=n + 1, dtype=BF16, scale=0.05)
+    b = randn(n, seed=k + 1, dtype=BF16)
+    ag, wg, bg = a.to(gpu), w.to(gpu), b.to(gpu)
+    out = cg.kernels._gemm(ag, wg, bg, epi, BF16, "t", tile=_lib.TILE_AUTO)
+    ref = gemm_ref(a, w, b, epi)
+    close(out, ref, 1e-3 * math.sqrt(k / 64), 2 ** -8, f"auto {m}x{n}x{k}")
+    alt = cg.kernels._gemm(ag, wg, bg, epi, BF16, "t", tile=15)
+    assert torch.equal(out, alt)
+
+
 @pytest.mark.parametrize("tile", range(5))
 @pytest.mark.parametrize("m,n,k", [(300, 520, 136), (512, 256, 768), (1, 50257, 64)])
 def test_gemm_every_bf16_tile(gpu, tile, m, n, k):
