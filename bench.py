@@ -75,7 +75,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="gpt2", choices=sorted(WORKLOADS) + ["xl-decode", "kernels"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seqs", type=int, default=2,
+    ap.add_argument("--cpu-seqs", type=int, default=8,
                     help="sequences (of seq_len tokens) per timed CPU-baseline forward")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after the run, copy a buffer of this many MiB 3 times (a kernel of "
