@@ -254,8 +254,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
           for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, s[qt][kt][r]);
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        mloc = column_max(mloc);
         const float mblk = mloc * scale_log2;  // scale > 0: max commutes
         const bool grow = mblk > m_run[qt] + kLazyLog2;
         if (__any(grow)) {
@@ -329,8 +328,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
   for (int qt = 0; qt < QT; ++qt) {
     const int qi = wave_q0 + qt * 16 + frow;
     float l = l_run[qt];
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    l = column_sum(l);
     if (qi >= Tq) continue;
     const float inv = l > 0.f ? 1.0f / l : 0.f;
     T* orow = O + b * o_sb + h * o_sh + qi * o_st;
@@ -526,8 +524,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_dma_kernel(
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
           for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, s[qt][kt][r]);
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        mloc = column_max(mloc);
         const float mblk = mloc * scale_log2;
         const bool grow = mblk > m_run[qt] + kLazyLog2;
         if (__any(grow)) {
@@ -579,8 +576,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_dma_kernel(
   for (int qt = 0; qt < QT; ++qt) {
     const int qi = wave_q0 + qt * 16 + frow;
     float l = l_run[qt];
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    l = column_sum(l);
     if (qi >= Tq) continue;
     const float inv = l > 0.f ? 1.0f / l : 0.f;
     bf16_t* orow = O + b * o_sb + h * o_sh + qi * o_st;

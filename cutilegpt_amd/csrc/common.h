@@ -126,6 +126,32 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
 }
 
+// Max / sum of lane i with lanes i ^ 16, i ^ 32 and i ^ 48 (one column across
+// the wave's four 16-lane rows), in every lane, through gfx950's
+// v_permlane16_swap / v_permlane32_swap: VALU moves between rows, no LDS round
+// trip.  Given the same value as both operands, a swap leaves in each lane the
+// pair {v[i], v[i ^ 16]} (resp. i ^ 32), in some order; max and + commute, so
+// all four lanes of a column end with the identical result.
+__device__ __forceinline__ float swap_combine16_max(float v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float swap_combine32_max(float v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float column_max(float v) {
+  return swap_combine32_max(swap_combine16_max(v));
+}
+__device__ __forceinline__ float column_sum(float v) {
+  auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
 
 // tanh-approximate GELU written through the identity
 //   0.5 x (1 + tanh(u)) = x / (1 + exp(-2u)),  u = sqrt(2/pi) (x + 0.044715 x^3),
