@@ -37,8 +37,8 @@ __device__ __forceinline__ u32x4_t gelu_vec16(const u32x4_t& raw) {
 }
 
 template <typename T>
-__global__ __launch_bounds__(kGeluThreads) void gelu_vec_kernel(const T* __restrict__ x,
-                                                                T* __restrict__ y,
+__global__ __launch_bounds__(kGeluThreads) void gelu_vec_kernel(const T* x,
+                                                                T* y,
                                                                 int64_t nvec) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int V = Elem<T>::kVec;
@@ -65,8 +65,8 @@ __global__ __launch_bounds__(kGeluThreads) void gelu_vec_kernel(const T* __restr
 
 // Scalar path for the ragged tail (and for unaligned tensors).
 template <typename T>
-__global__ __launch_bounds__(kGeluThreads) void gelu_scalar_kernel(const T* __restrict__ x,
-                                                                   T* __restrict__ y,
+__global__ __launch_bounds__(kGeluThreads) void gelu_scalar_kernel(const T* x,
+                                                                   T* y,
                                                                    int64_t begin, int64_t n) {
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kGeluThreads;
   for (int64_t i = begin + static_cast<int64_t>(blockIdx.x) * kGeluThreads + threadIdx.x; i < n;

@@ -81,7 +81,7 @@ __device__ __forceinline__ void decode_param(u32x4_t r, bool bf16, float* v) {
 // trip per wave, which is what short batches (decode steps) are bound by.
 template <typename TX, typename TD, typename TY, int NCH, int R, bool HASD, int POL>
 __global__ __launch_bounds__(kLnThreads) void add_layernorm_kernel(
-    const TX* __restrict__ x, const TD* __restrict__ delta, TX* x_out,
+    const TX* x, const TD* __restrict__ delta, TX* x_out,
     const void* __restrict__ gamma, const void* __restrict__ beta, bool param_bf16,
     TY* __restrict__ y, int64_t rows, int cols, float eps) {
   const int lane = threadIdx.x & 63;
@@ -372,7 +372,7 @@ template <> __device__ __forceinline__ float round_delta<bf16_t>(float v) { retu
 
 template <typename TD, typename TY, int MAXCH, int MAXP>
 __global__ __launch_bounds__(kLnpThreads) void add_layernorm_partials_kernel(
-    const float* __restrict__ x, const float* __restrict__ parts, int n_parts, int part_stride,
+    const float* x, const float* __restrict__ parts, int n_parts, int part_stride,
     int ldp, const void* __restrict__ bias, float* x_out, const void* __restrict__ gamma,
     const void* __restrict__ beta, bool param_bf16, TY* __restrict__ y, int cols, float eps) {
   __shared__ float scr[kLnpThreads / 64];

@@ -81,7 +81,7 @@ class DecodeSession:
         self.h = torch.empty((B, D), dtype=act, device=dev)
         self.qkv = torch.empty((B, 3 * D), dtype=act, device=dev)
         self.att = torch.empty((B, D), dtype=act, device=dev)
-        self.delta = torch.empty((B, D), dtype=act, device=dev)
+        self.delta = torch.empty((B, D), dtype=torch.float32, device=dev)
         self.f = torch.empty((B, 4 * D), dtype=act, device=dev)
         self.logits = torch.empty((B, V), dtype=model.logits_dtype, device=dev)
         self.err = torch.zeros(1, dtype=torch.int32, device=dev)
@@ -161,7 +161,7 @@ class DecodeSession:
         def add_ln(delta_ptr, wk, keep_x=True):
             chk(lib.cgpt_add_layernorm(px, delta_ptr, px if delta_ptr and keep_x else None,
                                        W[wk + ".weight"].data_ptr(), W[wk + ".bias"].data_ptr(),
-                                       ph, B, D, 1e-5, f32, ac, ac, ac, s), "add_layernorm")
+                                       ph, B, D, 1e-5, f32, f32, ac, ac, s), "add_layernorm")
 
         pp = self.parts.data_ptr()
 
@@ -176,7 +176,7 @@ class DecodeSession:
                                                 px if keep_x else None,
                                                 W[wk + ".weight"].data_ptr(),
                                                 W[wk + ".bias"].data_ptr(), ph, B, D, 1e-5, f32,
-                                                ac, ac, ac, s), "add_layernorm_partials")
+                                                f32, ac, ac, s), "add_layernorm_partials")
 
         chk(lib.cgpt_embedding_layernorm(self.ids.data_ptr(), W["wte"].data_ptr(),
                                          W["wpe"].data_ptr(), pstep, px,
@@ -213,12 +213,12 @@ class DecodeSession:
                                           3 * D, hd, 3 * D, hd, 3 * D, hd, csb, csh, cst, D, hd,
                                           scale, ac, self.err.data_ptr(), s), "attention_decode")
             gemm(pa, W[p + "attn.c_proj.weight"], W[p + "attn.c_proj.bias"], pd, D, D,
-                 _lib.EPI_BIAS, ac)
+                 _lib.EPI_BIAS, f32)
             add_ln(pd, p + "ln_2")
             gemm(ph, W[p + "mlp.c_fc.weight"], W[p + "mlp.c_fc.bias"], pf, 4 * D, D,
                  _lib.EPI_BIAS_GELU, ac)
             gemm(pf, W[p + "mlp.c_proj.weight"], W[p + "mlp.c_proj.bias"], pd, D, 4 * D,
-                 _lib.EPI_BIAS, ac)
+                 _lib.EPI_BIAS, f32)
             add_ln(pd, ln_next, keep_x=not last)
         gemm(ph, W["lm_head.weight"], None, self.logits.data_ptr(), V, D, _lib.EPI_NONE,
              _DT[self.logits.dtype], split=not self.partials)

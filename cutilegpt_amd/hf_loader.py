@@ -135,11 +135,15 @@ class HFWeightLoader:
             w, cfg = load_hf_checkpoint(self.model_name)
             self.config = dict(n_layer=cfg.n_layer, n_head=cfg.n_head, n_embd=cfg.n_embd)
             sd = internal_to_hf(w, cfg.n_layer)
-            try:
+            # GPT2LMHeadModel.state_dict() also lists the tied head.
+            sd["lm_head.weight"] = sd["transformer.wte.weight"]
+            # A tokenizer only when the directory holds its files (transformers
+            # would otherwise build an empty one).
+            self._tokenizer = None
+            files = set(os.listdir(self.model_name))
+            if "tokenizer.json" in files or {"vocab.json", "merges.txt"} <= files:
                 from transformers import GPT2TokenizerFast
                 self._tokenizer = GPT2TokenizerFast.from_pretrained(self.model_name)
-            except Exception:
-                self._tokenizer = None
         else:
             from transformers import GPT2LMHeadModel, GPT2Tokenizer
             model = GPT2LMHeadModel.from_pretrained(self.model_name)

@@ -246,18 +246,34 @@ def attention_qkv(qkv: torch.Tensor, n_head: int, out: Optional[torch.Tensor] = 
     transpose / ``ascontiguousarray`` glue around attention at
     ``cutile_gpt/models/gpt.py:133-146`` with strided addressing in the kernel.
     """
+    name = "attention_qkv"
+    _require_gpu(name, qkv, out)
+    _dtype_code(qkv, name)
+    if qkv.dim() != 3 or qkv.shape[2] % 3:
+        raise ValueError(f"{name}: qkv must be (B, T, 3*D), got {tuple(qkv.shape)}")
     B, T, D3 = qkv.shape
     D = D3 // 3
+    if n_head <= 0 or D % n_head:
+        raise ValueError(f"{name}: D={D} is not divisible by n_head={n_head}")
     hd = D // n_head
+    # Strides come from the tensor itself (a view such as qkv[:, :T2] keeps its
+    # parent's batch stride); the element axis must be contiguous.
+    sb, st_, se = qkv.stride()
+    if se != 1:
+        raise ValueError(f"{name}: the last axis of qkv must be contiguous")
     if out is None:
         out = torch.empty((B, T, D), dtype=qkv.dtype, device=qkv.device)
-    base = qkv
-    st = (T * D3, hd, D3)
-    q = base
-    k = base[..., D:]
-    v = base[..., 2 * D:]
+    elif out.shape != (B, T, D) or out.dtype != qkv.dtype or not out.is_contiguous():
+        raise ValueError(f"{name}: out must be a contiguous {qkv.dtype} tensor of shape "
+                         f"{(B, T, D)}, got {out.dtype} {tuple(out.shape)}")
+    elif out.device != qkv.device:
+        raise ValueError(f"{name}: out is on {out.device}, qkv on {qkv.device}")
+    st = (sb, hd, st_)
+    q = qkv
+    k = qkv[..., D:]
+    v = qkv[..., 2 * D:]
     _attention(q, k, v, out, B, n_head, T, T, hd, st, st, st, (T * D, hd, D),
-               1.0 / math.sqrt(hd), True, "attention_qkv")
+               1.0 / math.sqrt(hd), True, name)
     return out
 
 

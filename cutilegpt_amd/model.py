@@ -11,10 +11,11 @@ Forward data flow on one GPU (M = B*T rows, D = n_embd):
     h  (M, D)  act dtype  = LN1(x)                fused with layer 0's LayerNorm
     qkv(M, 3D) act dtype  = h Wqkv^T + b       <- MFMA GEMM, bias epilogue
     a  (M, D)  act dtype  = attention(qkv)     <- flash attention reading qkv strided
-    d  (M, D)  act dtype  = a Wo^T + b         <- GEMM
+    d  (M, D)  fp32       = a Wo^T + b         <- GEMM (fp32 out: the residual stream
+                                                  never takes a bf16-rounded delta)
     x += d ; h = LN2(x)                        <- fused add + LayerNorm
     f  (M, 4D) act dtype  = gelu(h Wfc^T + b)  <- GEMM with GELU epilogue
-    d          act dtype  = f Wp^T + b         <- GEMM
+    d          fp32       = f Wp^T + b         <- GEMM
     x += d ; h = LN1'(x) (next layer, or ln_f) <- fused add + LayerNorm
     logits (M, V) fp32    = h wte^T            <- GEMM (tied head, no bias)
 
@@ -194,7 +195,7 @@ class CutileGPT:
         h = torch.empty((M, D), dtype=act, device=dev)
         qkv = torch.empty((M, 3 * D), dtype=act, device=dev)
         att = torch.empty((M, D), dtype=act, device=dev)
-        delta = torch.empty((M, D), dtype=act, device=dev)
+        delta = torch.empty((M, D), dtype=torch.float32, device=dev)
         f = torch.empty((M, 4 * D), dtype=act, device=dev)
         Vp = self._head_pad.shape[0]
         logits = (torch.empty((M, Vp), dtype=self.logits_dtype, device=dev)
@@ -215,7 +216,7 @@ class CutileGPT:
             mark("ln", True)
             chk(lib.cgpt_add_layernorm(px, delta_ptr, px if delta_ptr and keep_x else None,
                                        W[wk + ".weight"].data_ptr(), W[wk + ".bias"].data_ptr(),
-                                       ph, M, D, 1e-5, f32, ac, ac, ac, s), "add_layernorm")
+                                       ph, M, D, 1e-5, f32, f32, ac, ac, s), "add_layernorm")
             mark("ln", False)
 
         # x = wte[idx] + wpe[pos] and h = ln_1(x) of layer 0 in one pass.
@@ -245,12 +246,12 @@ class CutileGPT:
                 "attention")
             mark("attention", False)
             gemm("gemm_proj", pa, W[p + "attn.c_proj.weight"], W[p + "attn.c_proj.bias"], pd,
-                 D, D, _lib.EPI_BIAS, ac)
+                 D, D, _lib.EPI_BIAS, f32)
             add_ln(pd, p + "ln_2")
             gemm("gemm_fc_gelu", ph, W[p + "mlp.c_fc.weight"], W[p + "mlp.c_fc.bias"], pf,
                  4 * D, D, _lib.EPI_BIAS_GELU, ac)
             gemm("gemm_mlp_proj", pf, W[p + "mlp.c_proj.weight"], W[p + "mlp.c_proj.bias"], pd,
-                 D, 4 * D, _lib.EPI_BIAS, ac)
+                 D, 4 * D, _lib.EPI_BIAS, f32)
             last = i + 1 == cfg.n_layer
             add_ln(pd, "ln_f" if last else f"h.{i + 1}.ln_1", keep_x=not last)
         if logits_out is not None:

@@ -18,11 +18,18 @@ How each function is pinned (checked against something other than itself):
 * ``causal_attention`` brute-force per-query loop, row 0 == V[0], equal keys
                        give the prefix mean of V, score-shift invariance,
                        ``torch.nn.functional.scaled_dot_product_attention``.
+* ``online_attention`` equal to ``causal_attention`` in float64 (the online
+                       form is exact algebra), with or without lazy rescaling;
+                       with P rounded to bf16 it equals the two-pass rounding
+                       where the first key block holds every row's maximum.
 * ``embedding``        exact gather vs indexing.
 * ``gpt_forward``      ``transformers.GPT2LMHeadModel`` (an installed library
                        implementation of the same architecture) with identical
                        weights, and the committed golden fixtures.
 * ``generate``         ``transformers`` greedy ``generate(do_sample=False)``.
+* ``forward_cached`` / ``generate_cached``  equal to ``gpt_forward`` / the
+                       full-recompute ``generate`` on small models (tokens and
+                       per-step logits).
 
 Nothing here is "parity unpinned" except the reference's own approximate GPU
 numerics (TF32 MMA, ``exp2(flush_to_zero)``, approximate division), which no
@@ -36,9 +43,12 @@ from .gpt_ref import (  # noqa: F401
     layer_norm,
     linear,
     causal_attention,
+    online_attention,
     embedding,
     gpt_forward,
+    forward_cached,
     generate,
+    generate_cached,
     init_weights,
     round_to,
 )

@@ -12,10 +12,15 @@ stored and in which dtype, so that the same restatement can model
                 (``kernels/linear.py:109``, ``kernels/layernorm.py:74``,
                 ``kernels/attention.py:109,115``), residual adds in bf16
                 (``models/gpt.py:155,174``), logits in bf16 (``linear.py:146``),
-* ``bf16``      the HIP path's flow: bf16 operands for every matrix product,
-                c_proj outputs stored bf16 (as the reference stores them) and
-                added to an fp32 residual stream, GELU fused into the
-                up-projection (one rounding), fp32 logits.
+                P rounded per 64-key block relative to the running maximum
+                (``kernels/attention.py:96-110``),
+* ``bf16``      the HIP path's flow: bf16 operands for every matrix product
+                (LN outputs, QKV, attention output, GELU output and P stored
+                bf16), c_proj outputs kept fp32 and added to an fp32 residual
+                stream, GELU fused into the up-projection (one rounding), fp32
+                logits, P rounded per 64-key block relative to a running
+                maximum that moves only when a block's maximum exceeds it by
+                more than 2^8 (the HIP kernel's lazy rescaling).
 
 Only ``tests/``, ``__graft_entry__.smoke`` and ``bench.py``'s CPU-baseline leg use
 this module.
@@ -46,6 +51,12 @@ class Flow:
     logits: torch.dtype       # storage of the logits
     p: torch.dtype            # dtype P is rounded to before the P.V product
     fused_gelu: bool          # GELU applied to the unrounded c_fc accumulator
+    # Where P is rounded (only matters when ``p`` is narrower than ``compute``):
+    # None = relative to each row's final maximum (two-pass softmax); a number
+    # = online softmax over 64-key blocks, relative to the running maximum,
+    # which moves to a block's maximum only when that exceeds it by more than
+    # this many powers of two (0: every increase, the reference's rule).
+    online_lazy: Optional[float] = None
 
 
 FLOWS: Dict[str, Flow] = {
@@ -54,9 +65,9 @@ FLOWS: Dict[str, Flow] = {
     "fp32": Flow("fp32", torch.float32, torch.float32, torch.float32, torch.float32,
                  torch.float32, torch.float32, False),
     "bf16_ref": Flow("bf16_ref", torch.float32, torch.bfloat16, torch.bfloat16,
-                     torch.bfloat16, torch.bfloat16, torch.bfloat16, False),
-    "bf16": Flow("bf16", torch.float32, torch.bfloat16, torch.float32, torch.bfloat16,
-                 torch.float32, torch.bfloat16, True),
+                     torch.bfloat16, torch.bfloat16, torch.bfloat16, False, 0.0),
+    "bf16": Flow("bf16", torch.float32, torch.bfloat16, torch.float32, torch.float32,
+                 torch.float32, torch.bfloat16, True, 8.0),
 }
 
 
@@ -104,8 +115,49 @@ def linear(x: torch.Tensor, weight: torch.Tensor,
     return y
 
 
+def online_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                     p_dtype: Optional[torch.dtype] = None, causal: bool = True,
+                     lazy_log2: float = 0.0, block: int = 64) -> torch.Tensor:
+    """Causal attention in the online (running-maximum) form of the kernel,
+    over key blocks of ``block`` keys taken in order.
+
+    Restates ``cutile_gpt/kernels/attention.py:80-116``: per block, scores are
+    scaled into the base-2 domain (scale / ln 2), the running maximum m moves to
+    max(m, block maximum), P = 2^(s - m) is summed unrounded into the
+    normaliser, rounded to the input dtype (``:109``) and multiplied with V;
+    earlier sums are rescaled by 2^(m_old - m_new); the result is divided by
+    the normaliser.  ``lazy_log2 > 0`` moves the maximum only when a block's
+    maximum exceeds it by more than that many powers of two (P then reaches
+    up to 2^lazy_log2; in exact arithmetic nothing changes).
+    """
+    hd = q.shape[-1]
+    t_q, t_k = q.shape[-2], k.shape[-2]
+    c = (1.0 / math.sqrt(hd)) / math.log(2.0)
+    s_all = q @ k.transpose(-1, -2)
+    if causal:
+        qi = torch.arange(t_q).unsqueeze(1) + (t_k - t_q)
+        kj = torch.arange(t_k).unsqueeze(0)
+        s_all = s_all.masked_fill(kj > qi, float("-inf"))
+    ninf = float("-inf")
+    m = torch.full(q.shape[:-1] + (1,), ninf, dtype=q.dtype)
+    l = torch.zeros_like(m)
+    acc = torch.zeros(q.shape[:-1] + (v.shape[-1],), dtype=q.dtype)
+    for j0 in range(0, t_k, block):
+        s = s_all[..., j0:j0 + block]
+        mblk = s.amax(-1, keepdim=True) * c
+        m_new = torch.where(mblk > m + lazy_log2, mblk, m) if lazy_log2 > 0 else torch.maximum(m, mblk)
+        alpha = torch.where(m == ninf, torch.zeros_like(m), torch.exp2(m - m_new))
+        p = torch.exp2(s * c - torch.where(m_new == ninf, torch.zeros_like(m_new), m_new))
+        l = l * alpha + p.sum(-1, keepdim=True)
+        if p_dtype is not None:
+            p = round_to(p, p_dtype)
+        acc = acc * alpha + p @ v[..., j0:j0 + block, :]
+        m = m_new
+    return acc / l
+
+
 def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                     p_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+                     p_dtype: Optional[torch.dtype] = None, causal: bool = True) -> torch.Tensor:
     """Causal softmax attention on (B, H, T, hd) tensors.
 
     Restates ``cutile_gpt/kernels/attention.py:24-116``: scores scaled by
@@ -113,7 +165,8 @@ def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     softmax over visible keys, P rounded to the input dtype before the P.V
     product (``:109``) while the normaliser sums unrounded P (``:100-103``).
     The online (running-max) formulation of the kernel is algebraically this
-    two-pass softmax.
+    two-pass softmax.  ``causal=False`` drops the mask (every query sees all
+    ``t_k`` keys), the unmasked case of the same kernel.
     """
     hd = q.shape[-1]
     t_q, t_k = q.shape[-2], k.shape[-2]
@@ -123,7 +176,8 @@ def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     # t_q == t_k; a decode step (t_q == 1) sees every cached key.
     qi = torch.arange(t_q).unsqueeze(1) + (t_k - t_q)
     kj = torch.arange(t_k).unsqueeze(0)
-    s = s.masked_fill(kj > qi, float("-inf"))
+    if causal:
+        s = s.masked_fill(kj > qi, float("-inf"))
     m = s.amax(-1, keepdim=True)
     p = torch.exp(s - m)
     l = p.sum(-1, keepdim=True)
@@ -150,6 +204,23 @@ def gpt_forward(w: Dict[str, torch.Tensor], idx: torch.Tensor, n_head: int,
     logits = ln_f(x) @ lm_head.weight.T with no LM-head bias.  ``w`` uses the
     reference's weight-dict keys (``models/gpt.py:45-81``), Linear weights (out, in).
     """
+    return forward_cached(w, idx, n_head, flow)[0]
+
+
+def forward_cached(w: Dict[str, torch.Tensor], idx: torch.Tensor, n_head: int,
+                   flow: Flow = FLOWS["fp32"], cache: Optional[list] = None):
+    """The forward of ``gpt_forward`` for tokens at positions p0 .. p0+T-1, where
+    p0 is the number of positions already held in ``cache`` (a list of per-layer
+    (k, v) tensors (B, H, p0, hd), stored in ``flow.act`` as the QKV projection
+    rounds them; None or empty for p0 = 0).  Returns (logits (B, T, V), the
+    cache extended by these T positions).
+
+    Every op but attention is row-local, and attention of a query at position p
+    reads only keys 0..p (``attention.py:90-94``), so running positions in two
+    parts with the earlier keys and values kept equals running them together:
+    this is the reference's full recompute (``models/gpt.py:204-206``) without
+    recomputing the prefix.
+    """
     c = flow.compute
 
     def W(key: str) -> torch.Tensor:
@@ -158,9 +229,11 @@ def gpt_forward(w: Dict[str, torch.Tensor], idx: torch.Tensor, n_head: int,
     B, T = idx.shape
     D = w["wte"].shape[1]
     hd = D // n_head
+    p0 = 0 if not cache else cache[0][0].shape[2]
+    new_cache = []
     # gpt.py:110-113
     tok = embedding(idx, W("wte"))
-    pos = embedding(torch.arange(T), W("wpe"))
+    pos = embedding(torch.arange(p0, p0 + T), W("wpe"))
     x = round_to(tok + pos.unsqueeze(0), flow.resid)
     for i in range(_n_layer(w)):
         p = f"h.{i}."
@@ -169,8 +242,16 @@ def gpt_forward(w: Dict[str, torch.Tensor], idx: torch.Tensor, n_head: int,
         qkv = round_to(linear(h, W(p + "attn.c_attn.weight"), W(p + "attn.c_attn.bias")), flow.act)
         q, k, v = qkv.split(D, dim=2)
         q, k, v = (t.reshape(B, T, n_head, hd).transpose(1, 2) for t in (q, k, v))
-        # gpt.py:140-155
-        a = round_to(causal_attention(q, k, v, flow.p), flow.act)
+        if cache:
+            k = torch.cat([cache[i][0], k], dim=2)
+            v = torch.cat([cache[i][1], v], dim=2)
+        new_cache.append((k, v))
+        # gpt.py:140-155 (queries at positions p0.., keys 0..p0+T-1)
+        if flow.online_lazy is None:
+            a = causal_attention(q, k, v, flow.p)
+        else:
+            a = online_attention(q, k, v, flow.p, lazy_log2=flow.online_lazy)
+        a = round_to(a, flow.act)
         a = a.transpose(1, 2).reshape(B, T, D)
         d = round_to(linear(a, W(p + "attn.c_proj.weight"), W(p + "attn.c_proj.bias")), flow.delta)
         x = round_to(x + d, flow.resid)
@@ -184,7 +265,7 @@ def gpt_forward(w: Dict[str, torch.Tensor], idx: torch.Tensor, n_head: int,
         x = round_to(x + d, flow.resid)
     # gpt.py:177-183
     h = round_to(layer_norm(x, W("ln_f.weight"), W("ln_f.bias")), flow.act)
-    return round_to(linear(h, W("lm_head.weight")), flow.logits)
+    return round_to(linear(h, W("lm_head.weight")), flow.logits), new_cache
 
 
 @torch.inference_mode()
@@ -203,6 +284,29 @@ def generate(w: Dict[str, torch.Tensor], idx: torch.Tensor, n_head: int, max_new
         nxt = logits.argmax(-1, keepdim=True)
         idx = torch.cat([idx, nxt], dim=1)
     return idx
+
+
+@torch.inference_mode()
+def generate_cached(w: Dict[str, torch.Tensor], idx: torch.Tensor, n_head: int,
+                    max_new_tokens: int, flow: Flow = FLOWS["fp32"],
+                    return_logits: bool = False):
+    """``generate`` (greedy) with the keys and values of earlier positions kept
+    (``forward_cached``) instead of re-running the whole prefix per token; the
+    prompt plus new tokens must fit the context (no cropping).  With
+    ``return_logits`` also returns the last-position logits of every step
+    (B, max_new_tokens, V)."""
+    out, seen = idx, []
+    logits, cache = forward_cached(w, idx, n_head, flow)
+    for t in range(max_new_tokens):
+        last = logits[:, -1, :]
+        seen.append(last)
+        nxt = last.argmax(-1, keepdim=True)
+        out = torch.cat([out, nxt], dim=1)
+        if t + 1 < max_new_tokens:
+            logits, cache = forward_cached(w, nxt, n_head, flow, cache)
+    if return_logits:
+        return out, torch.stack(seen, dim=1)
+    return out
 
 
 def init_weights(n_layer: int, n_head: int, n_embd: int, vocab_size: int = 50257,

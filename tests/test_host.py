@@ -137,3 +137,39 @@ def test_tile_table_lookup():
     n = _lib.load().cgpt_gemm_num_tiles()
     for key, t in tiles.TABLE.items():
         assert 0 <= t < n, key
+
+
+def test_sampling_semantics_temperature_and_top_k():
+    """CutileGPT._sample follows cutile_gpt/models/gpt.py:207-226: logits are
+    divided by the temperature, everything below the k-th largest is masked,
+    and the token is drawn from the softmax of the rest (top_k=1: the argmax).
+    Checked by drawing many samples from fixed logits on the CPU: every draw
+    lies in the top-k set and the frequencies match softmax(logits / T) over
+    that set within 5 standard errors."""
+    from cutilegpt_amd.model import CutileGPT
+    g = torch.Generator().manual_seed(0)
+    base = torch.randn(2, 40, generator=g) * 2.0
+    n = 40000
+    for temperature, top_k in ((0.7, 5), (1.5, 3), (1.0, None), (0.3, 40)):
+        torch.manual_seed(1)
+        logits = base.repeat_interleave(n, dim=0)
+        tok = CutileGPT._sample(logits, temperature, top_k).view(2, n)
+        for r in range(2):
+            z = base[r].double() / temperature
+            allowed = torch.ones_like(z, dtype=torch.bool)
+            if top_k is not None:
+                allowed = z >= torch.topk(z, top_k).values[-1]
+            p = torch.where(allowed, z, torch.tensor(float("-inf"), dtype=z.dtype)).softmax(-1)
+            assert allowed[tok[r]].all(), (temperature, top_k)
+            freq = torch.bincount(tok[r], minlength=40).double() / n
+            se = (p * (1 - p) / n).sqrt()
+            assert ((freq - p).abs() <= 5 * se + 1e-12).all(), (temperature, top_k)
+    # top_k = 1 is greedy whatever the temperature; a tiny temperature is too.
+    assert torch.equal(CutileGPT._sample(base, 3.0, 1).view(-1), base.argmax(-1))
+    assert torch.equal(CutileGPT._sample(base, 1e-6, None).view(-1), base.argmax(-1))
+
+
+def test_attention_qkv_rejects_host_tensors():
+    import cutilegpt_amd as cg
+    with pytest.raises(ValueError):
+        cg.attention_qkv(torch.zeros(1, 4, 3 * 64, dtype=torch.bfloat16), 2)

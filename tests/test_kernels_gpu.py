@@ -316,6 +316,70 @@ def test_attention_standalone_config(gpu, dtype):
     close(o, ref, *tol, f"attn standalone {dtype}")
 
 
+def _attn_raw(q, k, v, causal, scale=None):
+    """cgpt_attention_fwd on contiguous (B, H, T, hd) tensors, Tq = q rows, Tk = k rows."""
+    B, H, Tq, hd = q.shape
+    Tk = k.shape[2]
+    o = torch.empty_like(q)
+    lib = _lib.load()
+    code = {F32: _lib.CGPT_F32, BF16: _lib.CGPT_BF16}[q.dtype]
+    st = lambda t: t.stride()[:3]
+    _lib.check(lib.cgpt_attention_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), B, H,
+                                      Tq, Tk, hd, *st(q), *st(k), *st(v), *st(o),
+                                      1.0 / math.sqrt(hd) if scale is None else scale, int(causal),
+                                      code, torch.cuda.current_stream().cuda_stream), "attention")
+    return o
+
+
+@pytest.mark.parametrize("dtype", [BF16, F32])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("B,H,Tq,Tk,hd", [(1, 2, 1, 77, 64), (2, 3, 40, 200, 64),
+                                          (1, 2, 130, 130, 64), (2, 2, 65, 300, 128),
+                                          (1, 3, 17, 50, 32), (2, 1, 9, 9, 16),
+                                          (1, 2, 256, 512, 64)])
+def test_attention_tq_tk_and_non_causal(gpu, dtype, causal, B, H, Tq, Tk, hd):
+    """Query offset (Tk > Tq: query i at absolute position Tk - Tq + i) and the
+    unmasked case, in both kernels (bf16 hd 64/128 take the DMA kernel)."""
+    q = randn(B, H, Tq, hd, seed=31, dtype=dtype)
+    k, v = (randn(B, H, Tk, hd, seed=32 + i, dtype=dtype) for i in range(2))
+    o = _attn_raw(q.to(gpu), k.to(gpu), v.to(gpu), causal).cpu()
+    ref = R.causal_attention(q.double(), k.double(), v.double(),
+                             p_dtype=torch.bfloat16 if dtype == BF16 else None, causal=causal)
+    tol = (2e-5, 2e-5) if dtype == F32 else (4e-3, 2 ** -8)
+    close(o, ref, *tol, f"attn Tq={Tq} Tk={Tk} causal={causal}")
+
+
+def test_attention_qkv_rejects_bad_arguments(gpu):
+    x = torch.zeros(2, 8, 3 * 64, dtype=BF16, device=gpu)
+    with pytest.raises(ValueError):
+        cg.attention_qkv(x, 3)  # D = 64 not divisible by 3 heads
+    with pytest.raises(ValueError):
+        cg.attention_qkv(torch.zeros(2, 8, 100, dtype=BF16, device=gpu), 2)  # 3D not a multiple of 3
+    with pytest.raises(ValueError):
+        cg.attention_qkv(x, 2, out=torch.empty(2, 8, 32, dtype=BF16, device=gpu))  # wrong shape
+    with pytest.raises(ValueError):
+        cg.attention_qkv(x, 2, out=torch.empty(2, 8, 64, dtype=F32, device=gpu))  # wrong dtype
+    with pytest.raises(ValueError):
+        cg.attention_qkv(x, 2, out=torch.empty(2, 64, 8, dtype=BF16, device=gpu).transpose(1, 2))
+    with pytest.raises(ValueError):
+        cg.attention_qkv(x.cpu(), 2)
+    with pytest.raises(ValueError):
+        cg.attention_qkv(x.half(), 2)
+
+
+def test_attention_qkv_strided_view(gpu):
+    """A view of the first T2 positions of a longer buffer keeps its parent's
+    batch stride: the kernel must read it through qkv.stride(), not T2 * 3D."""
+    B, T, H, hd, T2 = 2, 96, 2, 64, 40
+    D = H * hd
+    full = randn(B, T, 3 * D, seed=41, dtype=BF16)
+    view = full.to(gpu)[:, :T2]
+    o = cg.attention_qkv(view, H).cpu()
+    q, k, v = (t.reshape(B, T2, H, hd).transpose(1, 2) for t in full[:, :T2].split(D, dim=2))
+    ref = attn_ref(q, k, v, BF16).transpose(1, 2).reshape(B, T2, D)
+    close(o, ref, 4e-3, 2 ** -8, "qkv strided view")
+
+
 def test_attention_row0_and_equal_keys(gpu):
     shape = (1, 2, 40, 64)
     q, k, v = (randn(*shape, seed=20 + i) for i in range(3))

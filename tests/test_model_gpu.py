@@ -4,12 +4,20 @@ and the golden fixture, at the benchmark configurations.
 Criteria (from the benchmark definition):
   fp32: max |logit error| <= 1e-3.
   bf16: max |logit error| <= 3e-2 against the exact (fp64) forward and against
-        the oracle's bf16 flow.  Top-1 agreement is measured and reported;
-        with random N(0, 0.02) weights the top-1/top-2 logit gap (~0.13) is
-        within ~50x of the bf16 rounding noise (~2e-3), so the oracle's own
-        bf16 flow run in fp32 vs fp64 arithmetic agrees on ~99.2% of positions.
-        The bound asserted here, >= 98.5% of all positions and every
-        last position, is what any bf16 implementation of this model can meet.
+        the oracle's bf16 flow (the HIP path's rounding points, fp32
+        arithmetic).  Top-1 agreement >= 99.9 % is not reachable between two
+        bf16 implementations of this model with random N(0, 0.02) weights: the
+        top-1/top-2 logit gap (~0.13) is within ~50x of the bf16 rounding
+        noise, so one flipped bf16 rounding anywhere upstream moves near-ties.
+        Measured on the CPU (medium config): the same bf16 flow in fp32 vs
+        fp64 arithmetic agrees on ~99.2 % of positions, and the three places
+        to round P in attention (two-pass, the reference's per-block online
+        rule, the kernel's lazy rescaling) agree pairwise on 98.4-98.9 %.
+        Asserted instead: top-1 agreement >= 98.5 % against both, 100 % at the
+        last position against fp64, every top-1 disagreement a near-tie (the
+        GPU's token scores within 3e-2 of the best under the oracle), and the
+        reference harness's ordered last-position top-5
+        (scripts/compare_mingpt.py:214-219) equal up to such near-ties.
 """
 
 import os
@@ -33,6 +41,21 @@ def make_model(cfg, w, dtype):
 
 def agreement(a, b):
     return (a.argmax(-1) == b.argmax(-1)).double().mean().item()
+
+
+def near_tie(out, ref):
+    """Largest ref.max - ref[argmax of out] over all positions: 0 where the
+    top-1 agrees, else how far the GPU's token is from the best under ref."""
+    a = out.argmax(-1, keepdim=True)
+    return (ref.amax(-1) - ref.gather(-1, a).squeeze(-1)).max().item()
+
+
+def top5_near_tie(out, ref):
+    """Largest |ref's r-th largest last-position logit - ref[out's r-th token]|
+    over ranks r < 5: 0 when the ordered top-5 lists are equal."""
+    idx = out[:, -1].topk(5, dim=-1).indices
+    vals = ref[:, -1].topk(5, dim=-1).values
+    return (vals - ref[:, -1].gather(-1, idx)).abs().max().item()
 
 
 def test_nano_fp32_vs_golden_and_oracle(gpu):
@@ -73,11 +96,25 @@ def check_bf16(m, w, ids, n_head, label, rows=None):
     agree_all = agreement(out, exact)
     agree_last = agreement(out[:, -1], exact[:, -1])
     ref_agree = agreement(flow, exact)
+    agree_flow = agreement(out, flow)
+    # Reference harness (scripts/compare_mingpt.py:214-219): ordered top-5 at
+    # the last position of every sequence.
+    top5 = lambda t: t[:, -1].topk(5, dim=-1).indices
+    top5_exact = torch.equal(top5(out), top5(exact))
+    top5_flow = torch.equal(top5(out), top5(flow))
+    tie_flow, tie_exact = near_tie(out, flow), near_tie(out, exact)
+    t5_flow, t5_exact = top5_near_tie(out, flow), top5_near_tie(out, exact)
     print(f"{label}: max|err| vs fp64 {e_exact:.3e}, vs bf16 flow {e_flow:.3e}; top-1 agree "
-          f"{agree_all * 100:.3f}% (oracle bf16 flow itself {ref_agree * 100:.3f}%), last pos "
-          f"{agree_last * 100:.1f}%")
+          f"vs bf16 flow {agree_flow * 100:.3f}%, vs fp64 {agree_all * 100:.3f}% (oracle bf16 "
+          f"flow itself vs fp64 {ref_agree * 100:.3f}%), last pos {agree_last * 100:.1f}%; "
+          f"largest near-tie taken {tie_flow:.2e} (flow) / {tie_exact:.2e} (fp64); last-position "
+          f"top-5 equal to fp64 {top5_exact}, to bf16 flow {top5_flow} (largest rank gap "
+          f"{t5_exact:.2e} / {t5_flow:.2e})")
     assert e_exact <= 3e-2 and e_flow <= 3e-2
-    assert agree_all >= 0.985 and agree_last == 1.0
+    assert agree_flow >= 0.985 and agree_all >= 0.985 and agree_last == 1.0
+    assert tie_flow <= 3e-2 and tie_exact <= 3e-2
+    assert t5_flow <= 3e-2 and t5_exact <= 3e-2
+    return agree_flow
 
 
 def test_medium_bf16(gpu):
@@ -125,3 +162,33 @@ def test_ragged_lengths_fp32(gpu):
         out = m(ids.to(gpu))[0].double().cpu()
         err = (out - R.gpt_forward(w, ids, 2, R.FLOWS["fp64"])).abs().max().item()
         assert err <= 1e-3, (T, err)
+
+
+def test_xl_bf16_prefill_all_positions(gpu):
+    """GPT-2 XL depth (48 layers, 25 heads, d 1600), the XL workload's b32 x 128
+    prompts in bf16: every position of rows 0 and 1 against the fp64 oracle and
+    the oracle's bf16 flow.  The projection outputs enter the fp32 residual
+    stream unrounded (with bf16-rounded deltas the oracle's flow reaches 0.029
+    here, unrounded 0.0245; the GPU measured 0.026): at 48 layers bf16 operands
+    for every matrix product leave ~15 % of the 3e-2 bar."""
+    from tests.golden.make_streams import prompts, weights
+    cfg = GPTConfig(n_layer=48, n_head=25, n_embd=1600, block_size=1024)
+    w = weights("xl")
+    m = CutileGPT(cfg, dtype=torch.bfloat16, init_weights=False)
+    m.load_weights(w)
+    ids = prompts()
+    logits, _ = m(ids.to(gpu))
+    out = logits[:2].double().cpu()
+    del logits, m
+    torch.cuda.empty_cache()
+    w32 = {k: v.float() for k, v in w.items()}
+    w32["lm_head.weight"] = w32["wte"]
+    del w
+    exact = R.gpt_forward(w32, ids[:2], 25, R.FLOWS["fp64"])
+    flow = R.gpt_forward(w32, ids[:2], 25, R.FLOWS["bf16"]).double()
+    e_exact = (out - exact).abs().max().item()
+    e_flow = (out - flow).abs().max().item()
+    print(f"XL b32x128 rows 0-1: max|err| vs fp64 {e_exact:.4f}, vs bf16 flow {e_flow:.4f}, "
+          f"oracle bf16 flow vs fp64 {(flow - exact).abs().max().item():.4f}; top-1 vs flow "
+          f"{agreement(out, flow) * 100:.2f}%, vs fp64 {agreement(out, exact) * 100:.2f}%")
+    assert e_exact <= 3e-2 and e_flow <= 3e-2

@@ -112,6 +112,25 @@ def test_attention_special_cases():
     torch.testing.assert_close(R.causal_attention(q, keq, v), prefix_mean)
     # a decode step (Tq = 1) equals the last row of the prefill
     torch.testing.assert_close(R.causal_attention(q[:, :, -1:], k, v), o[:, :, -1:])
+    # Tq < Tk: the queries are the last Tq rows of the Tk-row prefill
+    torch.testing.assert_close(R.causal_attention(q[:, :, -5:], k, v), o[:, :, -5:])
+
+
+def test_attention_non_causal_matches_sdpa_and_closed_forms():
+    g = torch.Generator().manual_seed(6)
+    q, k, v = (torch.randn(2, 3, 11, 16, dtype=torch.float64, generator=g) for _ in range(3))
+    o = R.causal_attention(q, k, v, causal=False)
+    torch.testing.assert_close(o, F.scaled_dot_product_attention(q, k, v, is_causal=False),
+                               rtol=1e-10, atol=1e-10)
+    # every query sees every key: equal keys give the plain mean of V in every row
+    keq = k[:, :, :1].expand_as(k)
+    torch.testing.assert_close(R.causal_attention(q, keq, v, causal=False),
+                               v.mean(2, keepdim=True).expand_as(v))
+    # Tq < Tk without the mask: the rows are those of the full query set
+    kk, vv = (torch.randn(2, 3, 19, 16, dtype=torch.float64, generator=g) for _ in range(2))
+    torch.testing.assert_close(R.causal_attention(q[:, :, :4], kk, vv, causal=False),
+                               F.scaled_dot_product_attention(q[:, :, :4], kk, vv),
+                               rtol=1e-10, atol=1e-10)
 
 
 def test_embedding_exact():
@@ -174,3 +193,77 @@ def test_bf16_flows_error_budget():
     for name in ("bf16", "bf16_ref"):
         d = (R.gpt_forward(w, ids, 4, R.FLOWS[name]).double() - exact).abs().max().item()
         assert d < 3e-2, (name, d)
+
+
+def test_forward_cached_in_parts_equals_one_pass():
+    """Positions run in parts with the earlier keys/values kept give the logits
+    of one pass over all positions (fp64: to rounding; bf16 flow: the same
+    rounding points, so the same values up to fp32 summation order)."""
+    w = R.init_weights(2, 4, 64, seed=12, dtype=torch.bfloat16, block_size=128)
+    ids = torch.randint(0, 50257, (3, 37), generator=torch.Generator().manual_seed(13))
+    for flow, tol in ((R.FLOWS["fp64"], 1e-10), (R.FLOWS["bf16"], 2e-2)):
+        full = R.gpt_forward(w, ids, 4, flow)
+        a, cache = R.forward_cached(w, ids[:, :20], 4, flow)
+        b, cache = R.forward_cached(w, ids[:, 20:33], 4, flow, cache)
+        c, cache = R.forward_cached(w, ids[:, 33:], 4, flow, cache)
+        assert cache[0][0].shape == (3, 4, 37, 16)
+        parts = torch.cat([a, b, c], dim=1)
+        assert (parts.double() - full.double()).abs().max().item() <= tol, flow.name
+        if flow.name == "fp64":
+            assert torch.equal(parts.argmax(-1), full.argmax(-1))
+
+
+@pytest.mark.parametrize("flow", ["fp64", "fp32", "bf16"])
+def test_generate_cached_equals_full_recompute(flow):
+    """The cached greedy loop (used to write the long-stream fixtures) gives the
+    full-recompute generate's tokens, and its per-step logits are the last rows
+    of a full forward over the produced sequence."""
+    f = R.FLOWS[flow]
+    w = R.init_weights(2, 2, 64, seed=14, dtype=torch.bfloat16 if flow == "bf16" else torch.float32)
+    ids = torch.randint(0, 50257, (2, 9), generator=torch.Generator().manual_seed(15))
+    ref = R.generate(w, ids, 2, 12, f)
+    out, lg = R.generate_cached(w, ids, 2, 12, f, return_logits=True)
+    assert torch.equal(out, ref)
+    full = R.gpt_forward(w, out[:, :-1], 2, f)[:, 8:]
+    tol = 1e-10 if flow == "fp64" else 2e-2
+    assert (lg.double() - full.double()).abs().max().item() <= tol
+
+
+def test_generate_cached_matches_golden_greedy():
+    gold = np.load(GOLDEN)
+    w = R.init_weights(3, 3, 48, seed=0)
+    out = R.generate_cached(w, torch.from_numpy(gold["greedy_prompt"]), 3, 8, R.FLOWS["fp64"])
+    np.testing.assert_array_equal(out.numpy(), gold["greedy_out"])
+
+
+@pytest.mark.parametrize("lazy", [0.0, 8.0])
+def test_online_attention_equals_two_pass(lazy):
+    """The online form is exact algebra: in float64 it equals the two-pass
+    softmax (causal, Tq < Tk, non-causal), lazy rescaling or not."""
+    g = torch.Generator().manual_seed(16)
+    q, k, v = (torch.randn(2, 3, 150, 16, dtype=torch.float64, generator=g) * 3 for _ in range(3))
+    for args in ((q, k, v), (q[:, :, 100:], k, v)):
+        torch.testing.assert_close(R.online_attention(*args, lazy_log2=lazy),
+                                   R.causal_attention(*args), rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(R.online_attention(q, k, v, causal=False, lazy_log2=lazy),
+                               R.causal_attention(q, k, v, causal=False), rtol=1e-12, atol=1e-12)
+
+
+def test_online_attention_rounding_point():
+    """Where key 0 carries every row's largest score, the running maximum is the
+    final one from the first block on, so P rounded to bf16 per block equals
+    P rounded after a two-pass softmax; where a later block raises the maximum,
+    the per-block rounding differs (it is relative to the running maximum)."""
+    g = torch.Generator().manual_seed(17)
+    q = torch.randn(1, 2, 200, 16, dtype=torch.float64, generator=g)
+    q[..., 0] = 5.0  # every query points along axis 0 ...
+    k = torch.randn(1, 2, 200, 16, dtype=torch.float64, generator=g) * 0.1
+    k[:, :, 0, 0] = 4.0  # ... and key 0 does too: the largest score of every row
+    v = torch.randn(1, 2, 200, 16, dtype=torch.float64, generator=g)
+    s = q @ k.transpose(-1, -2)
+    assert bool((s.argmax(-1) == 0).all())
+    bf = torch.bfloat16
+    torch.testing.assert_close(R.online_attention(q, k, v, bf), R.causal_attention(q, k, v, bf),
+                               rtol=1e-12, atol=1e-12)
+    k2 = torch.randn(1, 2, 200, 16, dtype=torch.float64, generator=g) * 2
+    assert (R.online_attention(q, k2, v, bf) - R.causal_attention(q, k2, v, bf)).abs().max() > 1e-6
