@@ -42,6 +42,8 @@ SIGNATURES = {
     "cgpt_gemm_skinny": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _I, _I,
                               _P, _I64, _P, _I64, _P]),
     "cgpt_gemm_skinny_workspace": (_I, [_I64, _I64, _I64, _I, _P, _P]),
+    "cgpt_gemm_skinny_noalloc": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I,
+                                      _I, _I, _P]),
     "cgpt_gemm_partials": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P]),
     "cgpt_gemm_partials_plan": (_I, [_I64, _I64, _I64, _I, _P]),
     "cgpt_attention_fwd": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,

@@ -9,6 +9,7 @@ extern "C" const char* cgpt_status_string(int status) {
     case CGPT_EINVAL: return "invalid argument (pointer, size, stride or alignment)";
     case CGPT_EDTYPE: return "unsupported dtype combination";
     case CGPT_ESHAPE: return "shape outside what the kernels support";
+    case CGPT_ESCRATCH: return "problem needs more scratch memory than the static buffer holds";
     default: break;
   }
   if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));

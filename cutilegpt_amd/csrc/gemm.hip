@@ -1462,9 +1462,9 @@ static int launch_epi(int epi, int tile, const void* a, const void* w, const voi
 extern "C" int cgpt_gemm_num_tiles(void) { return cgpt::kNumBf16Tiles; }
 
 namespace cgpt {
-// Argument checks shared by cgpt_gemm and cgpt_gemm_skinny: CGPT_OK when the
-// problem is well formed (M == 0 or N == 0 included: nothing to launch).
-static int validate_gemm(const void* a, const void* w, const void* bias, const void* c, int64_t M,
+// Argument checks shared by the GEMM entry points: CGPT_OK when the problem is
+// well formed (M == 0 or N == 0 included: nothing to launch).
+int validate_gemm(const void* a, const void* w, const void* bias, const void* c, int64_t M,
                          int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldc, int in_dtype,
                          int bias_dtype, int out_dtype, int epilogue) {
   if (M < 0 || N < 0 || K < 0) return CGPT_EINVAL;

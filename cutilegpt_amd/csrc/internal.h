@@ -6,6 +6,13 @@
 
 namespace cgpt {
 
+// Argument checks shared by the GEMM entry points (cgpt_gemm, the skinny
+// variants): CGPT_OK when the problem is well formed, M == 0 or N == 0
+// included (nothing to launch).
+int validate_gemm(const void* a, const void* w, const void* bias, const void* c, int64_t M,
+                  int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldc, int in_dtype,
+                  int bias_dtype, int out_dtype, int epilogue);
+
 // Skinny GEMM (M <= 64): C[M,N] = epilogue(A W^T + bias).  Column slices of
 // C, K split across the block's waves and (when workspace and counters are
 // given) across blocks.  Arguments as cgpt_gemm's, already validated

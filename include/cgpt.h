@@ -34,6 +34,7 @@ extern "C" {
 #define CGPT_EINVAL (-1)       /* bad pointer, size, stride or alignment */
 #define CGPT_EDTYPE (-2)       /* unsupported dtype combination */
 #define CGPT_ESHAPE (-3)       /* shape outside what the kernels support */
+#define CGPT_ESCRATCH (-4)     /* problem needs more than the static scratch holds */
 
 /* element types */
 #define CGPT_F32 0
@@ -139,6 +140,25 @@ int cgpt_gemm_skinny(const void* a, const void* w, const void* bias, void* c,
 /* Workspace bytes and counters cgpt_gemm_skinny needs for (M, N, K, in_dtype). */
 int cgpt_gemm_skinny_workspace(int64_t M, int64_t N, int64_t K, int in_dtype,
                                int64_t* workspace_bytes, int64_t* n_counters);
+
+/*
+ * cgpt_gemm_skinny with the split-K workspace and counters taken from a static
+ * device array of the library (8 MiB + 1024 ints per GPU, held until the
+ * process ends) instead of caller memory: allocates nothing (no hipMalloc,
+ * hipFree or allocating library call), so it can run under HIP graph capture
+ * and in loops that must not allocate.  No counterpart in the reference: it
+ * exists for callers that cannot allocate.  Same arguments, checks and result
+ * as cgpt_gemm_skinny given a workspace (bit-identical: the same kernels and
+ * split); a problem whose workspace would exceed the array returns
+ * CGPT_ESCRATCH (none with M <= 64 does).  The counters are cleared by a fill
+ * kernel on `stream` at every call.  Every call on a GPU uses that GPU's one
+ * array: calls that overlap in time on the same GPU (other streams or
+ * threads) race.
+ */
+int cgpt_gemm_skinny_noalloc(const void* a, const void* w, const void* bias, void* c,
+                             int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw,
+                             int64_t ldc, int in_dtype, int bias_dtype, int out_dtype,
+                             int epilogue, void* stream);
 
 /*
  * Split-K partial products of a decode-shaped GEMM (M <= 64), left for the

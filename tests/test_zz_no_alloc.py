@@ -1,0 +1,66 @@
+"""cgpt_gemm_skinny_noalloc (split-K skinny GEMM on the library's static
+scratch array) against cgpt_gemm_skinny with a caller workspace: bit-identical
+outputs on two calls in a row, the second with a smaller problem (the array
+keeps the first call's contents), plus the argument checks."""
+
+import ctypes
+
+import pytest
+import torch
+
+from cutilegpt_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_pair(gpu, M, N, K, epi, dtype, out_dtype):
+    lib = _lib.load()
+    s = torch.cuda.current_stream(gpu).cuda_stream
+    code = {torch.float32: _lib.CGPT_F32, torch.bfloat16: _lib.CGPT_BF16}
+    g = torch.Generator(device=gpu).manual_seed(M * 131 + N + K)
+    a = torch.randn(M, K, device=gpu, generator=g).to(dtype)
+    w = (torch.randn(N, K, device=gpu, generator=g) * 0.05).to(dtype)
+    b = torch.randn(N, device=gpu, generator=g).to(dtype)
+    wb, nc = ctypes.c_int64(), ctypes.c_int64()
+    _lib.check(lib.cgpt_gemm_skinny_workspace(M, N, K, code[dtype], ctypes.byref(wb),
+                                              ctypes.byref(nc)), "workspace")
+    ws = torch.empty(max(wb.value, 16) // 4 + 4, dtype=torch.float32, device=gpu)
+    cnt = torch.zeros(max(nc.value, 1), dtype=torch.int32, device=gpu)
+    ref = torch.full((M, N), float("nan"), dtype=out_dtype, device=gpu)
+    out = torch.full((M, N), float("nan"), dtype=out_dtype, device=gpu)
+    args = (a.data_ptr(), w.data_ptr(), b.data_ptr())
+    tail = (M, N, K, K, K, N, code[dtype], code[dtype], code[out_dtype], epi)
+    _lib.check(lib.cgpt_gemm_skinny(*args, ref.data_ptr(), *tail, ws.data_ptr(), wb.value,
+                                    cnt.data_ptr(), nc.value, s), "skinny")
+    _lib.check(lib.cgpt_gemm_skinny_noalloc(*args, out.data_ptr(), *tail, s), "skinny_noalloc")
+    torch.cuda.synchronize()
+    return out, ref, nc.value
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_noalloc_matches_workspace_path_twice(gpu, dtype):
+    """Two calls in a row, the second smaller: both bit-identical to the
+    caller-workspace path (same kernels, same split, same summation order)."""
+    for M, N, K, epi, od in ((32, 4800, 1600, _lib.EPI_BIAS, torch.float32),
+                             (7, 1600, 1280, _lib.EPI_BIAS_GELU, dtype)):
+        out, ref, n_counters = _run_pair(gpu, M, N, K, epi, dtype, od)
+        assert n_counters > 0  # the split-K path (workspace and counters) ran
+        assert torch.isfinite(out).all()
+        assert torch.equal(out, ref), (M, N, K)
+
+
+def test_noalloc_argument_checks(gpu):
+    lib = _lib.load()
+    x = torch.zeros(128, 128, dtype=torch.bfloat16, device=gpu)
+    p = x.data_ptr()
+    # M > 64: the skinny kernels take at most 64 rows
+    assert lib.cgpt_gemm_skinny_noalloc(p, p, None, p, 65, 64, 64, 64, 64, 64, 1, 1, 1, 0,
+                                        None) == -3
+    # K not a multiple of 8 for bf16; bias missing for a bias epilogue
+    assert lib.cgpt_gemm_skinny_noalloc(p, p, None, p, 4, 64, 60, 64, 64, 64, 1, 1, 1, 0,
+                                        None) == -3
+    assert lib.cgpt_gemm_skinny_noalloc(p, p, None, p, 4, 64, 64, 64, 64, 64, 1, 1, 1, 1,
+                                        None) == -1
+    assert lib.cgpt_gemm_skinny_noalloc(None, None, None, None, 0, 64, 64, 64, 64, 64, 1, 1, 1,
+                                        0, None) == 0
+    assert b"static buffer" in lib.cgpt_status_string(-4)
