@@ -180,8 +180,9 @@ def main():
         "gemm_mlp_proj": ("TFLOP/s", L * 2 * M * 4 * D * D),
         "lm_head": ("TFLOP/s", head_f),
         "attention": ("TFLOP/s", attn_f),
-        # add+LN: read x fp32 + delta bf16, write x fp32 + y bf16 (the last: no x write)
-        "ln": ("GB/s", (2 * L - 1) * M * D * (4 + 2 + 4 + 2) + M * D * (4 + 2 + 2)),
+        # LN: read x fp32, write y bf16 (the residual adds live in the projection
+        # GEMMs' epilogues)
+        "ln": ("GB/s", 2 * L * M * D * (4 + 2)),
         # gather + layer 0's LN: read wte + wpe rows bf16, write x fp32 + y bf16
         "embedding": ("GB/s", M * D * (2 + 2 + 4 + 2)),
     }

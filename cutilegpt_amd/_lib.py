@@ -23,6 +23,7 @@ CGPT_BF16 = 1
 EPI_NONE = 0
 EPI_BIAS = 1
 EPI_BIAS_GELU = 2
+EPI_BIAS_RESID = 3
 TILE_AUTO = -1
 TILE_SKINNY = -2
 

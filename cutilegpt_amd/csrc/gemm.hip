@@ -26,15 +26,11 @@
 //  * gemm_pipe_kernel: bf16 direct-to-LDS multi-stage pipeline, persistent
 //    over tiles (see the comment above it).
 #include "common.h"
+#include "gemm_common.h"
 #include "internal.h"
 
 namespace cgpt {
 
-#ifndef CGPT_GROUP_M
-#define CGPT_GROUP_M 8
-#endif
-constexpr int kGroupM = CGPT_GROUP_M;
-constexpr int kNumXcd = 8;
 
 #if defined(__HIP_DEVICE_COMPILE__)
 // Four consecutive outputs through a buffer resource: a store whose byte
@@ -57,21 +53,6 @@ __device__ __forceinline__ float load_bias(const void* bias, bool bf16, int64_t 
   return bf16 ? bf16_to_f32(static_cast<const bf16_t*>(bias)[n]) : static_cast<const float*>(bias)[n];
 }
 
-// Map a hardware block (or persistent tile) id to (tile_m, tile_n):
-// XCD-contiguous ranges of logical tiles, then groups of kGroupM tile rows.
-__device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
-  const int nblocks = tiles_m * tiles_n;
-  const int q = nblocks / kNumXcd, r = nblocks % kNumXcd;
-  const int xcd = bid % kNumXcd;
-  const int logical = xcd * q + (xcd < r ? xcd : r) + bid / kNumXcd;
-  const int group = kGroupM * tiles_n;
-  const int g = logical / group;
-  const int first_m = g * kGroupM;
-  const int gsz = min(tiles_m - first_m, kGroupM);
-  const int in_group = logical % group;
-  tm = first_m + in_group % gsz;
-  tn = in_group / gsz;
-}
 
 
 
@@ -226,6 +207,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(
         float t = acc[i][j][r];
         if (EPI != CGPT_EPI_NONE && n + r < N) t += load_bias(bias, bias_bf16, n + r);
         if (EPI == CGPT_EPI_BIAS_GELU) t = gelu_tanh(t);
+        if (EPI == CGPT_EPI_BIAS_RESID && n + r < N)
+          t += Elem<TOut>::load(C + static_cast<int64_t>(m) * ldc + n + r);
         v[r] = t;
       }
       TOut* out = C + static_cast<int64_t>(m) * ldc + n;
@@ -293,7 +276,6 @@ __device__ __forceinline__ void wait_stages(int later, bool stores) {
   wait_vmcnt<0>();
 }
 
-constexpr uint32_t kBufferRsrcWord3 = 0x00020000u;  // raw buffer, gfx9 family
 
 // Output modes of gemm_pipe_kernel.  kOutWaveStagedNT is kOutWaveStaged with
 // non-temporal stores: the LM head's logits (larger than the MALL, so nothing
@@ -892,7 +874,19 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_a3_kernel(
 // Output stores are non-temporal: in the GPT-2 forward this took c_attn from
 // 826 to 900 TFLOP/s and attn c_proj from 741 to 783, the attention that reads
 // c_attn's output lost 7 %, and the forward gained 1.2 %.
+//
+// Residual epilogue (CGPT_EPI_BIAS_RESID, fp32 C: C += A W^T + bias, the
+// residual stream of the model): the LDS that stages output rows otherwise
+// is a ring of residual fragments instead.  Each wave owns 24 16 x 16 blocks
+// of C (8 row blocks x 3 column blocks); the first 8 steps of a tile each add
+// one row block's 3 blocks of C into the accumulators (zero at the tile's
+// start), fetched two steps earlier by DMA in the accumulator layout (lane l's
+// 16 bytes land at slot + 16 l, so a linear ds_read_b128 returns them), and
+// the tile ends with direct buffer stores of the accumulators plus bias.  The
+// C reads are thereby spread over the K loop instead of serialising an
+// epilogue that would wait for them; requires K >= 512.
 constexpr int kSlabStorePolicy = 2;
+constexpr int kResidMinSteps = 8;  // k64 steps a tile needs for the residual ring
 
 template <int BM, int BN, int WGM, int WGN, int EPI, typename TOut>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_slab_kernel(
@@ -920,6 +914,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_slab_kernel(
   static_assert(IIP >= 1 && TM % IIP == 0, "output staging bands");
   static_assert(PASS_ROWS * CPRO == CH_PER_T * NT, "whole chunks per thread");
   static_assert(CPRO % 8 == 0, "rows of whole 128-byte groups");
+  constexpr bool RESID = EPI == CGPT_EPI_BIAS_RESID;
+  static_assert(!RESID || (sizeof(TOut) == 4 && TM == kResidMinSteps && TN == 3 &&
+                           NW * 2 * TN * 1024 <= OUT_BYTES),
+                "residual ring: fp32 C, 8 x 3 blocks a wave, two slots of 3 KiB a wave");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
   __shared__ __attribute__((aligned(16))) uint8_t sout[OUT_BYTES];
 
@@ -990,6 +988,33 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_slab_kernel(
     }
   };
 
+  // ---- residual ring (RESID): the C blocks of row block kt of a tile, for
+  // the tile's step kt < TM, go to slot (flat step & 1) of this wave, fetched
+  // at the middle of the step two flat steps earlier (the first two in the
+  // prologue), so the wait that precedes every step's second half — which
+  // leaves in flight at most an epilogue's stores and bias loads, issued after
+  // them — has retired them one step before they are read.
+  const u32x4_t rcres = buffer_desc(C, RESID ? static_cast<uint32_t>(
+                                               static_cast<int64_t>(M) * ldc * 4) : 0u);
+  uint8_t* const sres = sout + wave * (2 * TN * 1024);
+  int res_t = 0, res_kt = 0;  // tile and step of the next fetch
+  auto issue_res = [&]() {
+    if (res_t < n_mine && res_kt < TM) {
+      int tm, tn;
+      tile_of(res_t, tm, tn);
+      const int row = tm * BM + wm0 + res_kt * 16 + frow;
+      const int col = tn * BN + wn0 + 4 * fgrp;
+      const uint32_t base = static_cast<uint32_t>((static_cast<int64_t>(row) * ldc + col) * 4);
+      uint8_t* slot = sres + ((res_t * KT + res_kt) & 1) * (TN * 1024);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) dma_lds16(rcres, lds_addr(slot + j * 1024), base + j * 64, 0);
+    }
+    if (++res_kt == KT) {
+      res_kt = 0;
+      ++res_t;
+    }
+  };
+
   // ---- compute side
   f32x4_t acc[TM][TN];
   auto zero_acc = [&]() {
@@ -997,6 +1022,25 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_slab_kernel(
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  };
+  // Add row block kt's C blocks (slot of flat step g) into the accumulators.
+  auto add_res = [&](int kt, int g) {
+    if constexpr (RESID) {
+      const uint8_t* slot = sres + (g & 1) * (TN * 1024) + lane * 16;
+      f32x4_t r[TN];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) r[j] = *reinterpret_cast<const f32x4_t*>(slot + j * 1024);
+      switch (kt) {
+#define CGPT_RES_ROW(i) \
+  case i:               \
+    for (int j = 0; j < TN; ++j) acc[i][j] += r[j]; \
+    break;
+        CGPT_RES_ROW(0) CGPT_RES_ROW(1) CGPT_RES_ROW(2) CGPT_RES_ROW(3)
+        CGPT_RES_ROW(4) CGPT_RES_ROW(5) CGPT_RES_ROW(6) CGPT_RES_ROW(7)
+#undef CGPT_RES_ROW
+        default: break;
+      }
+    }
   };
   const int xo0 = (fgrp ^ (frow & 7)) << 4, xo1 = ((4 + fgrp) ^ (frow & 7)) << 4;
   const int a_base = (wm0 + frow) * ROWB, w_base = BM * ROWB + (wn0 + frow) * ROWB;
@@ -1062,6 +1106,26 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_slab_kernel(
     // stay live (and spill) through every K step.
     int zero;
     asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+    if constexpr (RESID) {
+      // Accumulators (C already added) plus bias, stored in place: exactly
+      // TM * TN stores (rows past M lie past the resource, column groups past
+      // N get an offset past it).
+#pragma unroll
+      for (int ii = 0; ii < TM; ++ii) {
+        const uint32_t roff = static_cast<uint32_t>((wm0 + ii * 16 + frow + zero) * ldc);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int n = n0 + wn0 + j * 16 + 4 * fgrp;
+          const u32x4_t d{__float_as_uint(acc[ii][j][0] + bias_at(j, 0)),
+                          __float_as_uint(acc[ii][j][1] + bias_at(j, 1)),
+                          __float_as_uint(acc[ii][j][2] + bias_at(j, 2)),
+                          __float_as_uint(acc[ii][j][3] + bias_at(j, 3))};
+          const uint32_t off = n < N ? (roff + static_cast<uint32_t>(n)) * 4u : 0x80000000u;
+          __builtin_amdgcn_raw_buffer_store_b128(d, rc, off, 0, 0);
+        }
+      }
+      return;
+    }
     const int lt = tid + zero, lrw = frow + zero;
 #pragma unroll
     for (int p = 0; p < NPASS; ++p) {
@@ -1114,9 +1178,14 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_slab_kernel(
 
   // Memory operations an epilogue leaves in flight: its stores and the next
   // tile's bias loads (capped to the counter's range: a stronger wait).
-  constexpr int EPI_OPS = vm_cap(NPASS * CH_PER_T + (EPI != CGPT_EPI_NONE ? TN : 0));
+  constexpr int EPI_OPS =
+      vm_cap((RESID ? TM * TN : NPASS * CH_PER_T) + (EPI != CGPT_EPI_NONE ? TN : 0));
   Frag f0, f1;
   if (EPI != CGPT_EPI_NONE) load_bias(0);
+  if (RESID) {
+    issue_res();
+    issue_res();
+  }
   issue(smem);
   if (total > 1) {
     issue(smem + STAGE);
@@ -1131,6 +1200,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_slab_kernel(
     zero_acc();
     for (int kt = 0; kt < KT; ++kt, ++g) {
       uint8_t* cur = smem + (g & 1) * STAGE;
+      if (RESID && kt < TM) add_res(kt, g);
       read_slab(cur, xo1, f1);
       mma_slab(f0);
       if (g + 1 < total) {
@@ -1140,6 +1210,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_slab_kernel(
           wait_vmcnt<0>();
         raw_barrier();
         if (g + 2 < total) issue(cur);
+        if (RESID) issue_res();
         // At a tile's last step the next slab is read after the epilogue,
         // so its fragments are not live across it.
         if (kt + 1 < KT) read_slab(smem + ((g + 1) & 1) * STAGE, xo0, f0);
@@ -1441,11 +1512,69 @@ static int auto_tile(bool bf16, int M, int N, int K, int64_t lda, int64_t ldw, i
   return last;
 }
 
+// Residual epilogue (C += A W^T + bias): the slab kernel's residual ring for
+// bf16 inputs into fp32 C where the problem suits it (at least 8 k64 steps,
+// whole 4-column groups, 32-bit offsets), else the register-staged kernel
+// with the tile the library's heuristic gives it.
+template <typename TIn, typename TOut>
+static int launch_resid(const void* a, const void* w, const void* bias, bool bias_bf16, void* c,
+                        int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc,
+                        bool vec_store, hipStream_t s) {
+  constexpr int EPI = CGPT_EPI_BIAS_RESID;
+  if constexpr (sizeof(TIn) == 2 && sizeof(TOut) == 4) {
+    const int64_t m = M, n = N;
+    if (K % 64 == 0 && K / 64 >= kResidMinSteps && n % 4 == 0 && ldc % 4 == 0 &&
+        reinterpret_cast<uintptr_t>(c) % 16 == 0 && (m + 256) * ldc * 4 < (int64_t{1} << 32) &&
+        (m + 256) * lda * 2 < (int64_t{1} << 32) && (n + 192) * ldw * 2 < (int64_t{1} << 32) &&
+        256 * ldc * 4 < 0x7fffffff) {
+      const int tiles_m = (M + 255) / 256, tiles_n = (N + 191) / 192;
+      const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
+      if (tiles > 0x7fffffff) return CGPT_ESHAPE;
+      const int grid = static_cast<int>(tiles < num_cus() ? tiles : num_cus());
+      hipLaunchKernelGGL((gemm_slab_kernel<256, 192, 2, 4, EPI, float>), dim3(grid), dim3(512), 0,
+                         s, static_cast<const bf16_t*>(a), static_cast<const bf16_t*>(w), bias,
+                         bias_bf16, static_cast<float*>(c), M, N, K, lda, ldw, ldc, tiles_m,
+                         tiles_n, vec_store);
+      return hip_status(hipGetLastError());
+    }
+  }
+  const TileCfg* t = sizeof(TIn) == 2 ? kBf16Tiles : kF32Tiles;
+  const int first = sizeof(TIn) == 2 ? (K >= 2048 ? 2 : 3) : 0;
+  const int last = sizeof(TIn) == 2 ? kFirstPipeTile - 1 : kNumF32Tiles - 1;
+  int tile = last;
+  for (int i = first; i <= last; ++i) {
+    if (static_cast<int64_t>((M + t[i].bm - 1) / t[i].bm) * ((N + t[i].bn - 1) / t[i].bn) >= 512) {
+      tile = i;
+      break;
+    }
+  }
+#define CGPT_RES_CFG(id, BM, BN)                                                                  \
+  case id:                                                                                        \
+    return launch_cfg<TIn, BM, BN, 2, 2, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda, ldw,  \
+                                                     ldc, vec_store, s);
+  if constexpr (sizeof(TIn) == 2) {
+    switch (tile) {
+      CGPT_RES_CFG(2, 128, 128)
+      CGPT_RES_CFG(3, 128, 64)
+      default: CGPT_RES_CFG(4, 64, 64)
+    }
+  } else {
+    switch (tile) {
+      CGPT_RES_CFG(0, 128, 128)
+      default: CGPT_RES_CFG(1, 64, 64)
+    }
+  }
+#undef CGPT_RES_CFG
+}
+
 template <typename TIn, typename TOut>
 static int launch_epi(int epi, int tile, const void* a, const void* w, const void* bias,
                       bool bias_bf16, void* c, int M, int N, int K, int64_t lda, int64_t ldw,
                       int64_t ldc, bool vec_store, hipStream_t s) {
   switch (epi) {
+    case CGPT_EPI_BIAS_RESID:
+      // Every tile id (and TILE_AUTO) takes the residual paths of launch_resid.
+      return launch_resid<TIn, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, s);
     case CGPT_EPI_NONE:
       return launch_tile<TIn, CGPT_EPI_NONE, TOut>(tile, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, s);
     case CGPT_EPI_BIAS:
@@ -1471,7 +1600,8 @@ int validate_gemm(const void* a, const void* w, const void* bias, const void* c,
   if (M == 0 || N == 0) return CGPT_OK;
   if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff) return CGPT_ESHAPE;
   if (a == nullptr || w == nullptr || c == nullptr) return CGPT_EINVAL;
-  if (epilogue != CGPT_EPI_NONE && epilogue != CGPT_EPI_BIAS && epilogue != CGPT_EPI_BIAS_GELU)
+  if (epilogue != CGPT_EPI_NONE && epilogue != CGPT_EPI_BIAS && epilogue != CGPT_EPI_BIAS_GELU &&
+      epilogue != CGPT_EPI_BIAS_RESID)
     return CGPT_EINVAL;
   if (epilogue != CGPT_EPI_NONE && bias == nullptr) return CGPT_EINVAL;
   if (in_dtype != CGPT_F32 && in_dtype != CGPT_BF16) return CGPT_EDTYPE;
@@ -1509,6 +1639,7 @@ extern "C" int cgpt_gemm_skinny(const void* a, const void* w, const void* bias, 
                                out_dtype, epilogue);
   if (st != CGPT_OK || M == 0 || N == 0) return st;
   if (M > 64) return CGPT_ESHAPE;
+  if (epilogue == CGPT_EPI_BIAS_RESID) return CGPT_EINVAL;  // not a skinny epilogue
   return launch_gemm_skinny(in_dtype == CGPT_BF16, epilogue, a, w, bias, bias_dtype == CGPT_BF16,
                             c, out_dtype == CGPT_BF16, static_cast<int>(M), static_cast<int>(N),
                             static_cast<int>(K), lda, ldw, ldc, workspace, workspace_bytes, counters,
@@ -1550,6 +1681,11 @@ extern "C" int cgpt_gemm(const void* a, const void* w, const void* bias, void* c
   if (st != CGPT_OK || M == 0 || N == 0) return st;
   const bool bf16 = in_dtype == CGPT_BF16;
   const int nt = bf16 ? kNumBf16Tiles : kNumF32Tiles;
+  if (epilogue == CGPT_EPI_BIAS_RESID) {
+    if (tile == CGPT_TILE_SKINNY) return CGPT_EINVAL;  // not a skinny epilogue
+    if (tile != CGPT_TILE_AUTO && (tile < 0 || tile >= nt)) return CGPT_EINVAL;
+    tile = 0;  // launch_resid picks the kernel
+  }
   if (tile == CGPT_TILE_AUTO && M <= 64) tile = CGPT_TILE_SKINNY;
   if (tile == CGPT_TILE_SKINNY) {
     if (M > 64) return CGPT_ESHAPE;

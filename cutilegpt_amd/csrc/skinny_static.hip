@@ -67,6 +67,7 @@ extern "C" int cgpt_gemm_skinny_noalloc(const void* a, const void* w, const void
                          epilogue);
   if (st != CGPT_OK || M == 0 || N == 0) return st;
   if (M > 64) return CGPT_ESHAPE;
+  if (epilogue == CGPT_EPI_BIAS_RESID) return CGPT_EINVAL;  // not a skinny epilogue
   const bool bf16 = in_dtype == CGPT_BF16;
   int64_t ws_bytes = 0, n_counters = 0;
   st = skinny_workspace(static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), bf16,

@@ -11,12 +11,13 @@ Forward data flow on one GPU (M = B*T rows, D = n_embd):
     h  (M, D)  act dtype  = LN1(x)                fused with layer 0's LayerNorm
     qkv(M, 3D) act dtype  = h Wqkv^T + b       <- MFMA GEMM, bias epilogue
     a  (M, D)  act dtype  = attention(qkv)     <- flash attention reading qkv strided
-    d  (M, D)  fp32       = a Wo^T + b         <- GEMM (fp32 out: the residual stream
-                                                  never takes a bf16-rounded delta)
-    x += d ; h = LN2(x)                        <- fused add + LayerNorm
+    x += a Wo^T + b                            <- GEMM with the residual add in its
+                                                  epilogue (fp32: the residual stream
+                                                  never takes a rounded delta)
+    h = LN2(x)                                 <- LayerNorm
     f  (M, 4D) act dtype  = gelu(h Wfc^T + b)  <- GEMM with GELU epilogue
-    d          fp32       = f Wp^T + b         <- GEMM
-    x += d ; h = LN1'(x) (next layer, or ln_f) <- fused add + LayerNorm
+    x += f Wp^T + b                            <- GEMM with the residual add
+    h = LN1'(x) (next layer, or ln_f)          <- LayerNorm
     logits (M, V) fp32    = h wte^T            <- GEMM (tied head, no bias)
 
 ``act dtype`` is the model dtype (float32 or bfloat16).  There is no CPU or
@@ -195,12 +196,11 @@ class CutileGPT:
         h = torch.empty((M, D), dtype=act, device=dev)
         qkv = torch.empty((M, 3 * D), dtype=act, device=dev)
         att = torch.empty((M, D), dtype=act, device=dev)
-        delta = torch.empty((M, D), dtype=torch.float32, device=dev)
         f = torch.empty((M, 4 * D), dtype=act, device=dev)
         Vp = self._head_pad.shape[0]
         logits = (torch.empty((M, Vp), dtype=self.logits_dtype, device=dev)
                   if logits_out is None else None)
-        px, ph, pq, pa, pd, pf = (t.data_ptr() for t in (x, h, qkv, att, delta, f))
+        px, ph, pq, pa, pf = (t.data_ptr() for t in (x, h, qkv, att, f))
 
         mark = probe if probe is not None else (lambda tag, start: None)
 
@@ -211,12 +211,12 @@ class CutileGPT:
                               M, n, k, k, w.stride(0), n, ac, ac, out_code, epi, t, s), tag)
             mark(tag, False)
 
-        def add_ln(delta_ptr, wk, keep_x=True):
-            # keep_x=False: the residual sum is not needed again (final LN).
+        def ln(wk):
+            # h = LayerNorm(x); x itself is left as it is.
             mark("ln", True)
-            chk(lib.cgpt_add_layernorm(px, delta_ptr, px if delta_ptr and keep_x else None,
-                                       W[wk + ".weight"].data_ptr(), W[wk + ".bias"].data_ptr(),
-                                       ph, M, D, 1e-5, f32, f32, ac, ac, s), "add_layernorm")
+            chk(lib.cgpt_add_layernorm(px, None, None, W[wk + ".weight"].data_ptr(),
+                                       W[wk + ".bias"].data_ptr(), ph, M, D, 1e-5, f32, f32, ac,
+                                       ac, s), "layernorm")
             mark("ln", False)
 
         # x = wte[idx] + wpe[pos] and h = ln_1(x) of layer 0 in one pass.
@@ -245,15 +245,15 @@ class CutileGPT:
                                        *st_qkv, *st_qkv, *st_qkv, *st_o, scale, 1, ac, s),
                 "attention")
             mark("attention", False)
-            gemm("gemm_proj", pa, W[p + "attn.c_proj.weight"], W[p + "attn.c_proj.bias"], pd,
-                 D, D, _lib.EPI_BIAS, f32)
-            add_ln(pd, p + "ln_2")
+            # x += att Wo^T + b (residual add in the GEMM epilogue, in place)
+            gemm("gemm_proj", pa, W[p + "attn.c_proj.weight"], W[p + "attn.c_proj.bias"], px,
+                 D, D, _lib.EPI_BIAS_RESID, f32)
+            ln(p + "ln_2")
             gemm("gemm_fc_gelu", ph, W[p + "mlp.c_fc.weight"], W[p + "mlp.c_fc.bias"], pf,
                  4 * D, D, _lib.EPI_BIAS_GELU, ac)
-            gemm("gemm_mlp_proj", pf, W[p + "mlp.c_proj.weight"], W[p + "mlp.c_proj.bias"], pd,
-                 D, 4 * D, _lib.EPI_BIAS, f32)
-            last = i + 1 == cfg.n_layer
-            add_ln(pd, "ln_f" if last else f"h.{i + 1}.ln_1", keep_x=not last)
+            gemm("gemm_mlp_proj", pf, W[p + "mlp.c_proj.weight"], W[p + "mlp.c_proj.bias"], px,
+                 D, 4 * D, _lib.EPI_BIAS_RESID, f32)
+            ln("ln_f" if i + 1 == cfg.n_layer else f"h.{i + 1}.ln_1")
         if logits_out is not None:
             # Last position of each sequence: rows b*T + T-1 of h, stride T*D.
             mark("lm_head", True)

@@ -44,6 +44,7 @@ extern "C" {
 #define CGPT_EPI_NONE 0        /* C = A W^T                                  */
 #define CGPT_EPI_BIAS 1        /* C = A W^T + bias                           */
 #define CGPT_EPI_BIAS_GELU 2   /* C = gelu_tanh(A W^T + bias)                */
+#define CGPT_EPI_BIAS_RESID 3  /* C = C + A W^T + bias (residual add in place) */
 
 /* ABI version (CGPT_ABI_VERSION) of the loaded library. */
 int cgpt_version(void);

@@ -479,3 +479,69 @@ def test_embedding_layernorm_device_position_and_clamp(gpu):
     assert err.item() == 1
     close(y, R.layer_norm(x.double().cpu(), g.double().cpu(), b.double().cpu()), 1e-5,
           2 ** -8 + 1e-5, "emb+ln decode")
+
+
+# ------------------------------------------------------ residual epilogue
+
+def _resid_gemm(a, w, b, c, tile=_lib.TILE_AUTO):
+    """c += a @ w.T + b through cgpt_gemm's residual epilogue (in place)."""
+    lib = _lib.load()
+    code = {F32: _lib.CGPT_F32, BF16: _lib.CGPT_BF16}
+    m, k = a.shape
+    n = w.shape[0]
+    _lib.check(lib.cgpt_gemm(a.data_ptr(), w.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k,
+                             a.stride(0), w.stride(0), c.stride(0), code[a.dtype], code[b.dtype],
+                             code[c.dtype], _lib.EPI_BIAS_RESID, tile,
+                             torch.cuda.current_stream().cuda_stream), "resid")
+
+
+@pytest.mark.parametrize("m,n,k", [(16384, 768, 768), (16384, 768, 3072), (4096, 512, 2048),
+                                   (4096, 1600, 1600), (300, 520, 512), (257, 192, 1024),
+                                   (1000, 200, 640), (513, 768, 4096)])
+def test_gemm_residual_epilogue_slab(gpu, m, n, k):
+    """C += A W^T + bias in place (bf16 A, W; fp32 C), the slab kernel's residual
+    ring where K gives it 8 k64 steps: against the fp64 sum; ragged M, N and
+    several tiles per block included."""
+    g = torch.Generator(device=gpu).manual_seed(m + n + k)
+    a = torch.randn(m, k, device=gpu, generator=g).to(BF16)
+    w = (torch.randn(n, k, device=gpu, generator=g) * 0.05).to(BF16)
+    b = torch.randn(n, device=gpu, generator=g).to(BF16)
+    x = torch.randn(m, n, device=gpu, generator=g) * 4
+    ref = x.double() + a.double() @ w.double().t() + b.double()
+    c = x.clone()
+    _resid_gemm(a, w, b, c)
+    err = (c.double() - ref).abs().max().item()
+    assert err <= 2e-4 * math.sqrt(k / 64), err
+
+
+@pytest.mark.parametrize("m,n,k,dt,ct", [(77, 130, 96, BF16, F32), (300, 96, 200, BF16, BF16),
+                                         (129, 64, 64, F32, F32), (64, 100, 1024, BF16, F32),
+                                         (16, 768, 768, BF16, F32), (5, 20, 40, F32, BF16)])
+def test_gemm_residual_epilogue_fallback(gpu, m, n, k, dt, ct):
+    """Shapes and types outside the residual ring (K below 512 or not a
+    multiple of 64, N not a multiple of 4, bf16 C, fp32 inputs, M <= 64) take
+    the register-staged kernel: C = C + A W^T + bias all the same."""
+    a = randn(m, k, seed=51, dtype=dt).to(gpu)
+    w = randn(n, k, seed=52, dtype=dt, scale=0.05).to(gpu)
+    b = randn(n, seed=53, dtype=dt).to(gpu)
+    x = randn(m, n, seed=54, scale=3.0).to(ct).to(gpu)
+    ref = x.double() + a.double() @ w.double().t() + b.double()
+    c = x.clone()
+    _resid_gemm(a, w, b, c)
+    tol = (2e-4, 1e-6) if ct == F32 else (4e-3, 2 ** -8)
+    close(c, ref, *tol, f"resid fallback {m}x{n}x{k}")
+
+
+def test_gemm_residual_epilogue_rejects_skinny(gpu):
+    lib = _lib.load()
+    x = torch.zeros(64, 64, device=gpu)
+    h = torch.zeros(64, 64, dtype=BF16, device=gpu)
+    p = h.data_ptr()
+    # explicit skinny tile / skinny entry points do not take the residual epilogue
+    assert lib.cgpt_gemm(p, p, p, x.data_ptr(), 8, 64, 64, 64, 64, 64, 1, 1, 0, 3,
+                         _lib.TILE_SKINNY, None) == -1
+    assert lib.cgpt_gemm_skinny(p, p, p, x.data_ptr(), 8, 64, 64, 64, 64, 64, 1, 1, 0, 3, None, 0,
+                                None, 0, None) == -1
+    # the residual epilogue needs a bias
+    assert lib.cgpt_gemm(p, p, None, x.data_ptr(), 8, 64, 64, 64, 64, 64, 1, 1, 0, 3, -1,
+                         None) == -1
