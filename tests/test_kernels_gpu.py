@@ -496,7 +496,7 @@ def _resid_gemm(a, w, b, c, tile=_lib.TILE_AUTO):
 
 
 @pytest.mark.parametrize("m,n,k", [(16384, 768, 768), (16384, 768, 3072), (4096, 512, 2048),
-                                   (4096, 1600, 1600), (300, 520, 512), (257, 192, 1024),
+                                   (4096, 1600, 1600), (300, 520, 512), (257, 192, 1024), (256, 384, 1536), (600, 200, 768),
                                    (1000, 200, 640), (513, 768, 4096)])
 def test_gemm_residual_epilogue_slab(gpu, m, n, k):
     """C += A W^T + bias in place (bf16 A, W; fp32 C), the slab kernel's residual
