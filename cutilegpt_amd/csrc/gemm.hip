@@ -1402,6 +1402,41 @@ static int launch_slab(const void* a, const void* w, const void* bias, bool bias
   return hip_status(hipGetLastError());
 }
 
+// Weight prefetch.  A persistent launch whose weight matrix is much larger
+// than an XCD's L2 (the LM heads: 50 257 x d_model) has every XCD sweep all
+// of W once per 8 tile rows, all eight XCDs at about the same column band at
+// the same time; when W has not been read recently the first touch of each
+// band comes from HBM at the start of a round and stalls the two-stage
+// pipeline.  Reading W once just before the GEMM leaves it in the 256 MiB
+// memory-side cache (MALL), from which all later band fetches are served.
+// The loads feed an empty asm so they are kept; nothing is stored.
+__global__ __launch_bounds__(256) void prefetch_kernel(const uint4* __restrict__ p, int64_t n) {
+  uint32_t x = 0;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) {
+    const uint4 v = p[i];
+    x ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  asm volatile("" ::"v"(x));
+}
+
+constexpr int64_t kPrefetchMinBytes = int64_t{32} << 20;  // W bytes that trigger it
+constexpr int kPrefetchMinTileRows = 4;                     // 256-row tile bands of A
+
+// Reads W (rows 0..N-1 of ldw bf16 elements, 16-byte aligned) ahead of a
+// persistent GEMM launch on the same stream when it is worth it.
+static int maybe_prefetch_w(const void* w, int64_t M, int64_t N, int64_t K, int64_t ldw,
+                            hipStream_t s) {
+  const int64_t bytes = ((N - 1) * ldw + K) * 2;
+  if (bytes < kPrefetchMinBytes || M < kPrefetchMinTileRows * 256 ||
+      reinterpret_cast<uintptr_t>(w) % 16 != 0)
+    return CGPT_OK;
+  const int64_t n = bytes / 16;  // whole 16-byte vectors inside W's extent
+  hipLaunchKernelGGL(prefetch_kernel, dim3(2048), dim3(256), 0, s,
+                     static_cast<const uint4*>(w), n);
+  return hip_status(hipGetLastError());
+}
+
 // The pipelined kernels address A and W through 32-bit buffer offsets and
 // consume K in whole stages.
 static bool pipe_ok(int tile, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) {
@@ -1703,6 +1738,10 @@ extern "C" int cgpt_gemm(const void* a, const void* w, const void* bias, void* c
   const bool vec_store = (ldc % 4 == 0) && (reinterpret_cast<uintptr_t>(c) % out_align == 0);
   const bool bias_bf16 = bias_dtype == CGPT_BF16;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (bf16 && tile >= kFirstPipeTile) {
+    const int pst = maybe_prefetch_w(w, M, N, K, ldw, s);
+    if (pst != CGPT_OK) return pst;
+  }
   const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
   if (bf16 && out_dtype == CGPT_BF16)
     return launch_epi<bf16_t, bf16_t>(epilogue, tile, a, w, bias, bias_bf16, c, m, n, k, lda, ldw, ldc, vec_store, s);
