@@ -19,7 +19,9 @@ events around every launch.
 ``standalone_kernels`` (also ``--workload kernels`` on its own): the standalone
 kernel set — tanh-GELU, LayerNorm and causal attention in fp32 and bf16 — each
 timed over rotating buffers larger than the MALL, as a fraction of its
-roofline.
+roofline; the HBM-bound ones also beside a plain device copy of the same bytes
+timed the same way (``copy_GB/s``, ``frac_of_copy``): the rate a copy reaches
+at 50-100 MB, well below the 8 TB/s peak.
 
 ``--workload xl-decode``: KV-cache greedy decoding of GPT-2 XL (48 layers, 25
 heads, d 1600), bf16 N(0, 0.02) weights generated on the device, batch 32,
@@ -400,6 +402,13 @@ def standalone_kernels(iters=40):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / iters
 
+    def copy_ceiling(xs, ys, nbytes):
+        # The ceiling a plain device copy reaches at the same byte count, timed
+        # the same way over the same rotating buffers (read nbytes / 2, write
+        # nbytes / 2): torch's copy of one tensor into another of its shape.
+        ms = timed(lambda i: ys[i].copy_(xs[i]), len(xs))
+        return round(nbytes / ms / 1e6, 1)
+
     def copies(t, pair_bytes):
         n = max(2, -(-ROTATE_BYTES // pair_bytes))
         return [t.clone() for _ in range(n)]
@@ -420,9 +429,12 @@ def standalone_kernels(iters=40):
         ms = timed(lambda i: _lib.check(lib.cgpt_gelu(xs[i].data_ptr(), ys[i].data_ptr(), n,
                                                       code[dt], s), "gelu"), len(xs))
         nbytes = 2 * n * es
+        copy = copy_ceiling(xs, ys, nbytes)
         out[f"gelu_{tag}"] = {"shape": [32, 512, 768], "avg_launch_ms": round(ms, 4),
                               "bytes": nbytes, "GB/s": round(nbytes / ms / 1e6, 1),
-                              "frac": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4), "bound": "hbm"}
+                              "frac": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4), "bound": "hbm",
+                              "copy_GB/s": copy,
+                              "frac_of_copy": round(nbytes / ms / 1e6 / copy, 4)}
         del xs, ys
         # LayerNorm: read x, write y, read gamma and beta.
         M, N = ln_x.shape
@@ -433,10 +445,12 @@ def standalone_kernels(iters=40):
             xs[i].data_ptr(), None, None, gw.data_ptr(), gb.data_ptr(), ys[i].data_ptr(), M, N,
             1e-5, code[dt], 0, code[dt], code[dt], s), "layernorm"), len(xs))
         nbytes = 2 * M * N * es + 2 * N * es
+        copy = copy_ceiling(xs, ys, 2 * M * N * es)
         out[f"layernorm_{tag}"] = {"shape": [M, N], "avg_launch_ms": round(ms, 4),
                                    "bytes": nbytes, "GB/s": round(nbytes / ms / 1e6, 1),
                                    "frac": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4),
-                                   "bound": "hbm"}
+                                   "bound": "hbm", "copy_GB/s": copy,
+                                   "frac_of_copy": round(nbytes / ms / 1e6 / copy, 4)}
         del xs, ys
         # Causal attention, (B, H, T, hd) contiguous: 4*B*H*hd*T(T+1)/2 FLOP.
         B, H, T, hd = qkv[0].shape
