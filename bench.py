@@ -36,6 +36,7 @@ alone.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -402,11 +403,19 @@ def standalone_kernels(iters=40):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / iters
 
+    blib = ctypes.CDLL(os.path.join(os.path.dirname(_lib.LIB_PATH), "libcgpt_bench.so"))
+    blib.cgpt_bench_copy16.restype = ctypes.c_int
+    blib.cgpt_bench_copy16.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                       ctypes.c_void_p]
+
     def copy_ceiling(xs, ys, nbytes):
-        # The ceiling a plain device copy reaches at the same byte count, timed
-        # the same way over the same rotating buffers (read nbytes / 2, write
-        # nbytes / 2): torch's copy of one tensor into another of its shape.
-        ms = timed(lambda i: ys[i].copy_(xs[i]), len(xs))
+        # The rate a plain device copy reaches at the same byte count (read
+        # nbytes / 2, write nbytes / 2), timed the same way over the same
+        # rotating buffers: 16 bytes a thread, non-temporal loads and stores.
+        def one(i):
+            if blib.cgpt_bench_copy16(xs[i].data_ptr(), ys[i].data_ptr(), nbytes // 2, s) != 0:
+                raise RuntimeError("cgpt_bench_copy16 failed")
+        ms = timed(one, len(xs))
         return round(nbytes / ms / 1e6, 1)
 
     def copies(t, pair_bytes):

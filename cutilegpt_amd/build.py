@@ -17,6 +17,7 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libcgpt.so")
+BENCH_LIB = os.path.join(HERE, "libcgpt_bench.so")
 ROOT = os.path.dirname(HERE)
 
 ARCH = "gfx950"
@@ -80,7 +81,25 @@ def build(verbose: bool = False, extra_flags=()) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
+    build_bench(extra_flags)
     return LIB
+
+
+def build_bench(extra_flags=()) -> str:
+    """``libcgpt_bench.so``: bench.py's bandwidth-ceiling probe (csrc_bench/),
+    kept out of libcgpt.so's ABI."""
+    src = os.path.join(HERE, "csrc_bench", "ceiling.hip")
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    obj = os.path.join(objdir, "bench_ceiling.o")
+    _compile(src, obj, list(extra_flags))
+    tmp = BENCH_LIB + ".tmp"
+    res = subprocess.run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, obj],
+                         capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link of libcgpt_bench.so failed:\n{res.stderr}")
+    os.replace(tmp, BENCH_LIB)
+    return BENCH_LIB
 
 
 if __name__ == "__main__":
