@@ -55,6 +55,12 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # profiles/lm_head_gemm_gpt2_traffic_pmc.md.  Only valid for the gpt2 workload.
 LM_HEAD_TRAFFIC_BYTES = 5.05e9
 
+# Kernel behind a persistent tile id (the LM head's roofline names it).
+TILE_KERNELS = {
+    14: "gemm_slab_kernel 256x192, fragment read-ahead, block-staged whole-line stores",
+    16: "gemm_pipe_kernel 256x256, wave-staged whole-line non-temporal stores",
+}
+
 WORKLOADS = {
     "gpt2": dict(n_layer=12, n_head=12, n_embd=768, batch=16, seq=1024,
                  name="gpt2-124m prefill b16xs1024"),
@@ -98,7 +104,7 @@ def main():
         return
 
     import torch
-    from cutilegpt_amd import CutileGPT, GPTConfig
+    from cutilegpt_amd import CutileGPT, GPTConfig, _lib
     from cutilegpt_amd.hf_loader import save_hf_checkpoint
 
     wl = WORKLOADS[args.workload]
@@ -213,8 +219,15 @@ def main():
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(w, ids, H, args.cpu_seqs)
 
+    from cutilegpt_amd.tiles import gemm_tile
+    Vp = model._head_pad.shape[0]
+    head_tile = gemm_tile(_lib.CGPT_BF16, B * T, Vp, D)
+    head_kernel = (f"lm_head GEMM (tile {head_tile}: {TILE_KERNELS.get(head_tile, 'library choice')}; "
+                   f"bf16 in, fp32 out, M={B * T}, N={V} padded to {Vp}, K={D})")
+    metric = ("prefill tok/s (GPT-2 124M, b16×s1024, bf16) + % of MFMA/HBM roofline"
+              if args.workload == "gpt2" else f"prefill tok/s ({wl['name']}, bf16)")
     line = {
-        "metric": "prefill tok/s (GPT-2 124M, b16×s1024, bf16) + % of MFMA/HBM roofline",
+        "metric": metric,
         "value": round(tok_s, 1),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -229,7 +242,7 @@ def main():
         "config": {"workload": wl["name"], "n_layer": L, "n_head": H, "n_embd": D,
                    "vocab_size": V, "batch": B, "seq_len": T, "logits": "fp32",
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "kernel": "lm_head GEMM (gemm_pipe_kernel 256x256, wave-staged whole-line non-temporal stores, bf16 in, fp32 out, N=50257 padded to 50304, K=768)",
+        "roofline": {"bound": "mfma", "kernel": head_kernel,
                      "achieved": round(head_tflops, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(head_tflops / PEAK_BF16_TFLOPS, 4),
                      "traffic": LM_HEAD_TRAFFIC_BYTES if args.workload == "gpt2" else None,
@@ -499,6 +512,27 @@ def bench_kernels(args):
     print(json.dumps(line), flush=True)
 
 
+def cpu_model() -> str:
+    """The host CPU's model name as lscpu reports it (``/proc/cpuinfo`` when
+    lscpu is absent)."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(w, ids, n_head, n_seqs):
     """CPU oracle fp32 forward (minGPT-architecture PyTorch) on the host cores:
     1 warmup + 3 timed forwards of ``n_seqs`` sequences, median."""
@@ -518,7 +552,7 @@ def cpu_baseline(w, ids, n_head, n_seqs):
             times.append(time.perf_counter() - t0)
     med = sorted(times)[1]
     return {"value": round(x.numel() / med, 1), "unit": "tok/s", "cores": threads,
-            "kind": "port",
+            "kind": "port", "cpu_model": cpu_model(),
             "sample": f"{n_seqs} x {x.shape[1]} tokens per forward, fp32, 1 warmup + 3 timed, median "
                       f"{med:.2f} s (oracle.gpt_ref.gpt_forward, torch threads={threads}, "
                       f"os.cpu_count()={os.cpu_count()})"}

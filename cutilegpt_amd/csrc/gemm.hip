@@ -1547,23 +1547,29 @@ static int auto_tile(bool bf16, int M, int N, int K, int64_t lda, int64_t ldw, i
   return last;
 }
 
-// Residual epilogue (C += A W^T + bias): the slab kernel's residual ring for
-// bf16 inputs into fp32 C where the problem suits it (at least 8 k64 steps,
-// whole 4-column groups, 32-bit offsets), else the register-staged kernel
-// with the tile the library's heuristic gives it.
+// Residual epilogue (C += A W^T + bias).  `tile`: 14 = the slab kernel's
+// residual ring (bf16 inputs into fp32 C, at least 8 k64 steps, whole
+// 4-column groups, 32-bit offsets; otherwise as TILE_AUTO); a register-staged
+// tile id (bf16 0-4, fp32 0-1) = that tile; anything else = TILE_AUTO: the
+// slab kernel when its 256x192 tiles give at least half the CUs a tile, else
+// the register-staged tile the library's heuristic gives (the largest with
+// 512 blocks, 64x64 below that).
 template <typename TIn, typename TOut>
-static int launch_resid(const void* a, const void* w, const void* bias, bool bias_bf16, void* c,
-                        int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc,
-                        bool vec_store, hipStream_t s) {
+static int launch_resid(int req_tile, const void* a, const void* w, const void* bias,
+                        bool bias_bf16, void* c, int M, int N, int K, int64_t lda, int64_t ldw,
+                        int64_t ldc, bool vec_store, hipStream_t s) {
   constexpr int EPI = CGPT_EPI_BIAS_RESID;
+  const int last = sizeof(TIn) == 2 ? kFirstPipeTile - 1 : kNumF32Tiles - 1;
+  const bool reg_tile = req_tile >= 0 && req_tile <= last;
   if constexpr (sizeof(TIn) == 2 && sizeof(TOut) == 4) {
     const int64_t m = M, n = N;
-    if (K % 64 == 0 && K / 64 >= kResidMinSteps && n % 4 == 0 && ldc % 4 == 0 &&
+    const int tiles_m = (M + 255) / 256, tiles_n = (N + 191) / 192;
+    const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
+    const bool want = req_tile == 14 || (!reg_tile && 2 * tiles >= num_cus());
+    if (want && K % 64 == 0 && K / 64 >= kResidMinSteps && n % 4 == 0 && ldc % 4 == 0 &&
         reinterpret_cast<uintptr_t>(c) % 16 == 0 && (m + 256) * ldc * 4 < (int64_t{1} << 32) &&
         (m + 256) * lda * 2 < (int64_t{1} << 32) && (n + 192) * ldw * 2 < (int64_t{1} << 32) &&
         256 * ldc * 4 < 0x7fffffff) {
-      const int tiles_m = (M + 255) / 256, tiles_n = (N + 191) / 192;
-      const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
       if (tiles > 0x7fffffff) return CGPT_ESHAPE;
       const int grid = static_cast<int>(tiles < num_cus() ? tiles : num_cus());
       hipLaunchKernelGGL((gemm_slab_kernel<256, 192, 2, 4, EPI, float>), dim3(grid), dim3(512), 0,
@@ -1575,12 +1581,16 @@ static int launch_resid(const void* a, const void* w, const void* bias, bool bia
   }
   const TileCfg* t = sizeof(TIn) == 2 ? kBf16Tiles : kF32Tiles;
   const int first = sizeof(TIn) == 2 ? (K >= 2048 ? 2 : 3) : 0;
-  const int last = sizeof(TIn) == 2 ? kFirstPipeTile - 1 : kNumF32Tiles - 1;
   int tile = last;
-  for (int i = first; i <= last; ++i) {
-    if (static_cast<int64_t>((M + t[i].bm - 1) / t[i].bm) * ((N + t[i].bn - 1) / t[i].bn) >= 512) {
-      tile = i;
-      break;
+  if (reg_tile) {
+    tile = req_tile;
+  } else {
+    for (int i = first; i <= last; ++i) {
+      if (static_cast<int64_t>((M + t[i].bm - 1) / t[i].bm) * ((N + t[i].bn - 1) / t[i].bn) >=
+          512) {
+        tile = i;
+        break;
+      }
     }
   }
 #define CGPT_RES_CFG(id, BM, BN)                                                                  \
@@ -1589,6 +1599,8 @@ static int launch_resid(const void* a, const void* w, const void* bias, bool bia
                                                      ldc, vec_store, s);
   if constexpr (sizeof(TIn) == 2) {
     switch (tile) {
+      CGPT_RES_CFG(0, 256, 256)
+      CGPT_RES_CFG(1, 256, 128)
       CGPT_RES_CFG(2, 128, 128)
       CGPT_RES_CFG(3, 128, 64)
       default: CGPT_RES_CFG(4, 64, 64)
@@ -1608,8 +1620,8 @@ static int launch_epi(int epi, int tile, const void* a, const void* w, const voi
                       int64_t ldc, bool vec_store, hipStream_t s) {
   switch (epi) {
     case CGPT_EPI_BIAS_RESID:
-      // Every tile id (and TILE_AUTO) takes the residual paths of launch_resid.
-      return launch_resid<TIn, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, s);
+      return launch_resid<TIn, TOut>(tile, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc,
+                                     vec_store, s);
     case CGPT_EPI_NONE:
       return launch_tile<TIn, CGPT_EPI_NONE, TOut>(tile, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, s);
     case CGPT_EPI_BIAS:
@@ -1719,7 +1731,19 @@ extern "C" int cgpt_gemm(const void* a, const void* w, const void* bias, void* c
   if (epilogue == CGPT_EPI_BIAS_RESID) {
     if (tile == CGPT_TILE_SKINNY) return CGPT_EINVAL;  // not a skinny epilogue
     if (tile != CGPT_TILE_AUTO && (tile < 0 || tile >= nt)) return CGPT_EINVAL;
-    tile = 0;  // launch_resid picks the kernel
+    // launch_resid picks the kernel (tile: a preference).
+    const int64_t out_align = out_dtype == CGPT_F32 ? 16 : 8;
+    const bool vec_store = (ldc % 4 == 0) && (reinterpret_cast<uintptr_t>(c) % out_align == 0);
+    const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool bb = bias_dtype == CGPT_BF16;
+    if (bf16 && out_dtype == CGPT_BF16)
+      return launch_resid<bf16_t, bf16_t>(tile, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, s);
+    if (bf16)
+      return launch_resid<bf16_t, float>(tile, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, s);
+    if (out_dtype == CGPT_F32)
+      return launch_resid<float, float>(tile, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, s);
+    return launch_resid<float, bf16_t>(tile, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, s);
   }
   if (tile == CGPT_TILE_AUTO && M <= 64) tile = CGPT_TILE_SKINNY;
   if (tile == CGPT_TILE_SKINNY) {

@@ -30,10 +30,16 @@ Tile ids index the configuration table compiled into libcgpt.so
                c_fc + GELU)
     fp32: 0 = 128x128, 1 = 64x64
 
-``TABLE`` maps exact (dtype, M, N, K) problems measured on MI355X to the tile
-that won; anything else falls back to the library's own heuristic
+``TABLE`` maps (dtype, M bucket, N, K) to the tile that won a sweep of every
+tile on MI355X (``python -m cutilegpt_amd.tune``: each model's prefill GEMMs,
+bias / GELU / residual epilogues and output types as the forward runs them).
+The M bucket is the power of two at or above M, so one entry covers every M
+in (bucket / 2, bucket] — batch x sequence products that differ a little share
+a choice.  Anything else falls back to the library's own heuristic
 (``TILE_AUTO``: the persistent tile that fills the 256 CUs best, else the
-register-staged kernel's largest tile giving every CU about two blocks).
+register-staged kernel's largest tile giving every CU about two blocks).  For
+the residual epilogue (attn / MLP c_proj into the fp32 residual stream) a
+tile id picks between the slab kernel (14) and the register-staged tiles.
 """
 
 from __future__ import annotations
@@ -42,24 +48,38 @@ from typing import Dict, Tuple
 
 from . import _lib
 
-# (dtype code, M, N, K) -> tile id.  Winners of an event-timed sweep of every
-# tile on MI355X (bias epilogue, bf16 out); TFLOP/s of the winner in comments.
+
+def m_bucket(m: int) -> int:
+    """The power of two at or above ``m`` (1 for m <= 1)."""
+    return 1 << max(0, (int(m) - 1).bit_length())
+
+
+# (dtype code, M bucket, N, K) -> tile id, from the sweep (TFLOP/s of the
+# winner, inputs hot; attn/MLP c_proj with the residual epilogue, fp32 out).
 _B = _lib.CGPT_BF16
 TABLE: Dict[Tuple[int, int, int, int], int] = {
     # GPT-2 124M prefill, M = 16 x 1024
-    (_B, 16384, 2304, 768): 14,   # c_attn       981
-    (_B, 16384, 768, 768): 14,    # attn c_proj  841
-    (_B, 16384, 3072, 768): 16,   # c_fc + GELU   947 in the forward (858 on id 15)
-    (_B, 16384, 768, 3072): 14,   # mlp c_proj  1202
-    (_B, 16384, 50304, 768): 16,  # lm head (vocab padded), fp32 out 963
-    # 'medium' (8L, d 512) prefill, M = 16 x 256
-    (_B, 4096, 1536, 512): 14,    # 431
-    (_B, 4096, 2048, 512): 10,    # 520 (GELU epilogue)
-    (_B, 4096, 512, 2048): 4,     # 361
-    (_B, 4096, 50304, 512): 16,   # lm head (vocab padded), fp32 out
+    (_B, 16384, 2304, 768): 14,   # c_attn        988
+    (_B, 16384, 768, 768): 14,    # attn c_proj   616 (register tiles <= 303)
+    (_B, 16384, 3072, 768): 16,   # c_fc + GELU   976
+    (_B, 16384, 768, 3072): 14,   # mlp c_proj   1002
+    (_B, 16384, 50304, 768): 16,  # lm head (vocab padded), fp32 out  991
+    # 'medium' (8 layers, d 512) prefill, M = 16 x 256
+    (_B, 4096, 1536, 512): 14,    # c_attn        463
+    (_B, 4096, 512, 512): 4,      # attn c_proj   161 (64x64: 512 blocks; slab 102)
+    (_B, 4096, 2048, 512): 10,    # c_fc + GELU   520
+    (_B, 4096, 512, 2048): 4,     # mlp c_proj    286 (slab 181)
+    (_B, 4096, 50304, 512): 16,   # lm head       801
+    # GPT-2 XL (48 layers, d 1600) prefill inside generate, M = 32 x 128
+    (_B, 4096, 4800, 1600): 14,   # c_attn        961
+    (_B, 4096, 1600, 1600): 14,   # attn c_proj   479
+    (_B, 4096, 6400, 1600): 16,   # c_fc + GELU   929
+    (_B, 4096, 1600, 6400): 14,   # mlp c_proj    658
+    (_B, 4096, 50304, 1600): 16,  # lm head      1076
 }
 
 
 def gemm_tile(dtype_code: int, m: int, n: int, k: int) -> int:
-    """Tile id for a GEMM problem (exact table hit, else the library heuristic)."""
-    return TABLE.get((dtype_code, m, n, k), _lib.TILE_AUTO)
+    """Tile id for a GEMM problem (table hit for M's bucket, else the library
+    heuristic)."""
+    return TABLE.get((dtype_code, m_bucket(m), n, k), _lib.TILE_AUTO)

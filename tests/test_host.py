@@ -137,6 +137,14 @@ def test_tile_table_lookup():
     n = _lib.load().cgpt_gemm_num_tiles()
     for key, t in tiles.TABLE.items():
         assert 0 <= t < n, key
+        assert tiles.m_bucket(key[1]) == key[1], key  # keys hold bucket values
+    # one entry covers every M of its bucket, (bucket / 2, bucket]
+    assert tiles.m_bucket(1) == 1 and tiles.m_bucket(4096) == 4096
+    assert tiles.m_bucket(4097) == 8192 and tiles.m_bucket(2049) == 4096
+    bf = _lib.CGPT_BF16
+    assert tiles.gemm_tile(bf, 16384, 2304, 768) == tiles.gemm_tile(bf, 8200, 2304, 768) == 14
+    assert tiles.gemm_tile(bf, 8192, 2304, 768) == _lib.TILE_AUTO
+    assert tiles.gemm_tile(bf, 3000, 512, 512) == 4
 
 
 def test_sampling_semantics_temperature_and_top_k():

@@ -505,8 +505,8 @@ def _resid_gemm(a, w, b, c, tile=_lib.TILE_AUTO):
                                    (1000, 200, 640), (513, 768, 4096)])
 def test_gemm_residual_epilogue_slab(gpu, m, n, k):
     """C += A W^T + bias in place (bf16 A, W; fp32 C), the slab kernel's residual
-    ring where K gives it 8 k64 steps: against the fp64 sum; ragged M, N and
-    several tiles per block included."""
+    ring (tile 14) where K gives it 8 k64 steps: against the fp64 sum; ragged M,
+    N and several tiles per block included."""
     g = torch.Generator(device=gpu).manual_seed(m + n + k)
     a = torch.randn(m, k, device=gpu, generator=g).to(BF16)
     w = (torch.randn(n, k, device=gpu, generator=g) * 0.05).to(BF16)
@@ -514,7 +514,26 @@ def test_gemm_residual_epilogue_slab(gpu, m, n, k):
     x = torch.randn(m, n, device=gpu, generator=g) * 4
     ref = x.double() + a.double() @ w.double().t() + b.double()
     c = x.clone()
-    _resid_gemm(a, w, b, c)
+    _resid_gemm(a, w, b, c, tile=14)
+    err = (c.double() - ref).abs().max().item()
+    assert err <= 2e-4 * math.sqrt(k / 64), err
+
+
+@pytest.mark.parametrize("tile", [_lib.TILE_AUTO, 0, 1, 2, 3, 4, 9])
+@pytest.mark.parametrize("m,n,k", [(4096, 512, 2048), (300, 520, 512), (513, 200, 640)])
+def test_gemm_residual_epilogue_tiles(gpu, tile, m, n, k):
+    """The residual epilogue on every register-staged tile a planner may ask for
+    (and TILE_AUTO, which takes the register kernel when 256x192 slab tiles
+    would leave most CUs idle; a persistent tile id other than 14 means
+    TILE_AUTO): C = C + A W^T + bias against the fp64 sum."""
+    g = torch.Generator(device=gpu).manual_seed(m + 7 * n + k + tile)
+    a = torch.randn(m, k, device=gpu, generator=g).to(BF16)
+    w = (torch.randn(n, k, device=gpu, generator=g) * 0.05).to(BF16)
+    b = torch.randn(n, device=gpu, generator=g).to(BF16)
+    x = torch.randn(m, n, device=gpu, generator=g) * 4
+    ref = x.double() + a.double() @ w.double().t() + b.double()
+    c = x.clone()
+    _resid_gemm(a, w, b, c, tile=tile)
     err = (c.double() - ref).abs().max().item()
     assert err <= 2e-4 * math.sqrt(k / 64), err
 
