@@ -53,7 +53,7 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # Bytes beyond L2 per LM-head launch (2.0 x FETCH_SIZE + 1.0 x WRITE_SIZE, factors from
 # a 1 GiB copy), measured with rocprofv3 --pmc on the GPT-2 workload; see
 # profiles/lm_head_gemm_gpt2_traffic_pmc.md.  Only valid for the gpt2 workload.
-LM_HEAD_TRAFFIC_BYTES = 5.05e9
+LM_HEAD_TRAFFIC_BYTES = 5.15e9
 
 # Kernel behind a persistent tile id (the LM head's roofline names it).
 TILE_KERNELS = {

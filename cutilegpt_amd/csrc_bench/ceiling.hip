@@ -6,7 +6,7 @@
 
 #include <cstdint>
 
-namespace {
+namespace cgpt_bench {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -16,7 +16,7 @@ __global__ __launch_bounds__(256) void copy16_nt_kernel(const u32x4* __restrict_
   if (i < n) __builtin_nontemporal_store(__builtin_nontemporal_load(x + i), y + i);
 }
 
-}  // namespace
+}  // namespace cgpt_bench
 
 // Copies `bytes` (a multiple of 16; x and y 16-byte aligned) from x to y on
 // `stream`.  Returns 0, or -1 for bad arguments, or the HIP error code.
@@ -28,8 +28,8 @@ extern "C" int cgpt_bench_copy16(const void* x, void* y, int64_t bytes, void* st
   if (n == 0) return 0;
   const int64_t blocks = (n + 255) / 256;
   if (blocks > 0x7fffffff) return -1;
-  hipLaunchKernelGGL(copy16_nt_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const u32x4*>(x),
-                     static_cast<u32x4*>(y), n);
+  hipLaunchKernelGGL(cgpt_bench::copy16_nt_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const cgpt_bench::u32x4*>(x),
+                     static_cast<cgpt_bench::u32x4*>(y), n);
   return static_cast<int>(hipGetLastError());
 }
