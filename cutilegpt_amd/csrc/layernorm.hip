@@ -175,8 +175,8 @@ __global__ __launch_bounds__(kLnThreads) void add_layernorm_kernel(
 // over the 32 lanes of the half (DPP rows of 16, then the two rows' results).
 template <int NCH>
 __global__ __launch_bounds__(kLnThreads) void layernorm_bf16_rows16_kernel(
-    const bf16_t* __restrict__ x, const bf16_t* __restrict__ gamma,
-    const bf16_t* __restrict__ beta, bf16_t* __restrict__ y, int64_t rows, int cols, float eps) {
+    const bf16_t* x, const bf16_t* __restrict__ gamma, const bf16_t* __restrict__ beta,
+    bf16_t* y, int64_t rows, int cols, float eps) {
   const int lane = threadIdx.x & 63, hl = lane & 31;
   const int64_t wrow = (static_cast<int64_t>(blockIdx.x) * kLnRowsPerBlock + (threadIdx.x >> 6)) * 2;
   if (wrow >= rows) return;
