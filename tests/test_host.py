@@ -181,3 +181,19 @@ def test_attention_qkv_rejects_host_tensors():
     import cutilegpt_amd as cg
     with pytest.raises(ValueError):
         cg.attention_qkv(torch.zeros(1, 4, 3 * 64, dtype=torch.bfloat16), 2)
+
+
+def test_tune_shapes_cover_the_table():
+    """The sweep's shapes are the forward's GEMMs (c_attn, attn c_proj, c_fc,
+    MLP c_proj, padded LM head) per config, and every TABLE entry is one of
+    them at its M bucket."""
+    from cutilegpt_amd import tune, tiles, _lib
+    got = set()
+    for name, (d, m) in tune.CONFIGS.items():
+        sh = tune.shapes(name)
+        assert [s[0] for s in sh] == ["c_attn", "attn_c_proj", "c_fc_gelu", "mlp_c_proj", "lm_head"]
+        assert [(s[2], s[3]) for s in sh] == [(3 * d, d), (d, d), (4 * d, d), (d, 4 * d),
+                                              (tune.VOCAB_PAD, d)]
+        assert sh[1][4] == sh[3][4] == _lib.EPI_BIAS_RESID and sh[2][4] == _lib.EPI_BIAS_GELU
+        got |= {(_lib.CGPT_BF16, tiles.m_bucket(s[1]), s[2], s[3]) for s in sh}
+    assert set(tiles.TABLE) <= got

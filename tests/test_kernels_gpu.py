@@ -287,6 +287,24 @@ def test_gemm_gpt2_shapes_vs_torch(gpu, n, k):
     assert err < 2e-4 * math.sqrt(k / 64), err
 
 
+@pytest.mark.parametrize("tile", [14, 16])
+def test_gemm_weight_prefetch_strided_w(gpu, tile):
+    """A persistent launch over a weight matrix past the prefetch threshold
+    (>= 32 MiB, M >= 1024), with W rows padded (ldw > K): the read ahead of the
+    GEMM covers exactly W's extent and the product is unchanged (against
+    torch's fp32 matmul of the same bf16 operands)."""
+    m, n, k, ldw = 1024, 21000, 768, 832
+    g = torch.Generator(device=gpu).manual_seed(5)
+    a = torch.randn(m, k, device=gpu, generator=g).to(BF16)
+    wbig = (torch.randn(n, ldw, device=gpu, generator=g) * 0.02).to(BF16)
+    w = wbig[:, :k]
+    assert ((n - 1) * ldw + k) * 2 >= 32 << 20
+    out = cg.kernels._gemm(a, w, None, _lib.EPI_NONE, F32, "t", tile=tile)
+    ref = a.float() @ w.float().t()
+    err = (out - ref).abs().max().item()
+    assert err < 2e-4 * math.sqrt(k / 64), err
+
+
 # ---------------------------------------------------------------- Attention
 
 ATTN_SHAPES = [(1, 1, 1, 64), (1, 2, 5, 16), (2, 3, 17, 32), (1, 1, 130, 64), (2, 4, 64, 64),
