@@ -167,7 +167,8 @@ __global__ __launch_bounds__(kLnThreads) void add_layernorm_kernel(
   }
 }
 
-// bf16 rows in and out, no residual, bf16 gamma / beta, cols % 8 == 0: a
+// bf16 rows in and out, no residual, bf16 gamma / beta, cols % 8 == 0 and
+// cols <= 2048 (141 VGPRs a lane at 2048; 4096 would leave one wave a SIMD): a
 // half-wave (32 lanes) per row so every access is 16 bytes (8 elements), the
 // width at which a plain streaming copy runs fastest; with 4 elements a lane
 // (8-byte accesses) the 16384 x 768 launch moved 4.1 TB/s.  Lane h of a half
@@ -258,8 +259,7 @@ static int launch_ln_bf16_rows16(const bf16_t* x, const bf16_t* gamma, const bf1
   else if (cols <= 768) CGPT_LN16(3);
   else if (cols <= 1024) CGPT_LN16(4);
   else if (cols <= 1792) CGPT_LN16(7);
-  else if (cols <= 2048) CGPT_LN16(8);
-  else CGPT_LN16(16);
+  else CGPT_LN16(8);
 #undef CGPT_LN16
   return hip_status(hipGetLastError());
 }
@@ -620,7 +620,7 @@ extern "C" int cgpt_add_layernorm(const void* x, const void* delta, void* x_out,
   const bool pb = param_dtype == CGPT_BF16;
   const int c = static_cast<int>(cols);
   if (x_dtype == CGPT_BF16 && y_dtype == CGPT_BF16 && pb && delta == nullptr &&
-      x_out == nullptr && c % 8 == 0 &&
+      x_out == nullptr && c % 8 == 0 && c <= 2048 &&
       ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15) == 0)
     return launch_ln_bf16_rows16(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(gamma),
                                  static_cast<const bf16_t*>(beta), static_cast<bf16_t*>(y), rows,
