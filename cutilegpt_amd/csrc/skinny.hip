@@ -33,7 +33,12 @@ namespace cgpt {
 struct SkShape {
   int nt, nw, dpw;
 };
-constexpr SkShape kSkShapes[] = {{2, 8, 1}, {4, 8, 2}, {2, 16, 2}};
+// Shape 3 (8 n-tiles, 4 waves, 1 double slab a round) is for wide N with the
+// final epilogue: 128 columns a block halve the A re-reads of shape 1 and
+// its 4-wave blocks leave LDS for more of them a CU (GPT-2 XL LM head, 32
+// rows: 60 -> 50 us on weights rotated past the MALL; as the partials
+// shape for K = 6400 it was slower, 8.1 -> 10.2 us).
+constexpr SkShape kSkShapes[] = {{2, 8, 1}, {4, 8, 2}, {2, 16, 2}, {8, 4, 1}};
 constexpr int kSkTargetBlocks = 512;  // fix-up path: blocks to aim for
 constexpr int kSkMaxSplit = 16;       // fix-up path: K chunks per column slice at most
 constexpr int kCpolSc1 = 16;          // buffer cache-policy bits: sc1 (agent scope)
@@ -247,7 +252,9 @@ static SkinnyPlan skinny_plan(int M, int N, int K, int elem_bytes, bool have_ws)
   if (have_ws) {
     p.shape = 0;
   } else if (slices2 >= 1024) {
-    p.shape = 1;  // wide N (an LM head): fewer A re-reads per weight byte
+    // wide N (an LM head): fewer A re-reads per weight byte; shape 3 holds
+    // 8 n-tiles of accumulators, so four m-tiles stay on shape 1
+    p.shape = p.mt < 4 ? 3 : 1;
   } else {
     // 16 waves leave 128 VGPRs a lane: too few for four m-tiles' fragments.
     p.shape = p.dslabs >= 16 && p.mt < 4 ? 2 : 0;
@@ -305,8 +312,10 @@ static void launch_shape(const SkinnyPlan& p, const TIn* A, const TIn* W, const 
       p, A, W, bias, bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s)
   if (p.shape == 1) {
     CGPT_SK_SHAPE(1);
-  } else if constexpr (MT < 4) {  // the planners never give shape 2 four m-tiles
-    if (p.shape == 2)
+  } else if constexpr (MT < 4) {  // the planners give shapes 2 and 3 at most two m-tiles
+    if (p.shape == 3)
+      CGPT_SK_SHAPE(3);
+    else if (p.shape == 2)
       CGPT_SK_SHAPE(2);
     else
       CGPT_SK_SHAPE(0);

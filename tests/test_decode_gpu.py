@@ -30,7 +30,8 @@ def stream(dev):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("M,N,K", [(1, 16, 64), (5, 50, 72), (16, 1600, 1600), (17, 96, 256),
                                    (32, 4800, 1600), (33, 70, 520), (64, 200, 6400),
-                                   (32, 50257, 64)])
+                                   (32, 50257, 64), (32, 50257, 1600), (17, 40000, 1600),
+                                   (8, 33000, 200), (64, 32800, 128)])
 @pytest.mark.parametrize("epi", [_lib.EPI_NONE, _lib.EPI_BIAS, _lib.EPI_BIAS_GELU])
 def test_skinny_gemm_vs_fp64(gpu, dtype, M, N, K, epi):
     g = torch.Generator().manual_seed(M * 7919 + N * 31 + K)
