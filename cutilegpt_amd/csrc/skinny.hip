@@ -38,7 +38,10 @@ struct SkShape {
 // its 4-wave blocks leave LDS for more of them a CU (GPT-2 XL LM head, 32
 // rows: 60 -> 50 us on weights rotated past the MALL; as the partials
 // shape for K = 6400 it was slower, 8.1 -> 10.2 us).
-constexpr SkShape kSkShapes[] = {{2, 8, 1}, {4, 8, 2}, {2, 16, 2}, {8, 4, 1}};
+// Shape 4 (4 n-tiles, 4 waves, 1 double slab) takes the partials of long K
+// (>= 64 double slabs: MLP-proj at K = 6400, 7.8-8.1 -> 7.4 us in a sweep of
+// every shape over weights rotated past the MALL).
+constexpr SkShape kSkShapes[] = {{2, 8, 1}, {4, 8, 2}, {2, 16, 2}, {8, 4, 1}, {4, 4, 1}};
 constexpr int kSkTargetBlocks = 512;  // fix-up path: blocks to aim for
 constexpr int kSkMaxSplit = 16;       // fix-up path: K chunks per column slice at most
 constexpr int kCpolSc1 = 16;          // buffer cache-policy bits: sc1 (agent scope)
@@ -282,11 +285,11 @@ static SkinnyPlan partials_plan(int M, int N, int K, int elem_bytes, int split) 
   const int kd = 8 * (16 / elem_bytes);
   p.mt = sk_mt(M);
   p.dslabs = (K + kd - 1) / kd;
-  p.shape = p.dslabs >= 64 ? 1 : 0;
+  p.shape = p.dslabs >= 64 ? 4 : 0;
   const SkShape& s = kSkShapes[p.shape];
   p.slices = (N + 16 * s.nt - 1) / (16 * s.nt);
   if (split <= 0) {
-    const int target = p.shape == 1 ? 10 : 5;
+    const int target = p.shape == 4 ? 10 : 5;
     split = (p.dslabs + target - 1) / target;
   }
   p.split = split;
@@ -312,6 +315,8 @@ static void launch_shape(const SkinnyPlan& p, const TIn* A, const TIn* W, const 
       p, A, W, bias, bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s)
   if (p.shape == 1) {
     CGPT_SK_SHAPE(1);
+  } else if (p.shape == 4) {
+    CGPT_SK_SHAPE(4);
   } else if constexpr (MT < 4) {  // the planners give shapes 2 and 3 at most two m-tiles
     if (p.shape == 3)
       CGPT_SK_SHAPE(3);
