@@ -20,6 +20,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcgpt.so"
 
 CGPT_F32 = 0
 CGPT_BF16 = 1
+CGPT_F16 = 2
 EPI_NONE = 0
 EPI_BIAS = 1
 EPI_BIAS_GELU = 2

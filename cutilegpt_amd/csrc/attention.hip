@@ -41,6 +41,12 @@ template <> struct AttnMfma<bf16_t> {
                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
   }
 };
+template <> struct AttnMfma<f16_t> {
+  __device__ static void run(const u32x4_t& a, const u32x4_t& b, f32x4_t& c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                               __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+};
 template <> struct AttnMfma<float> {
   __device__ static void run(const u32x4_t& a, const u32x4_t& b, f32x4_t& c) {
 #pragma unroll
@@ -53,6 +59,10 @@ template <> struct AttnMfma<float> {
 __device__ __forceinline__ void store4_o(float* p, const float* v) { store_vec(p, v); }
 __device__ __forceinline__ void store4_o(bf16_t* p, const float* v) {
   u32x2_t u = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  *reinterpret_cast<u32x2_t*>(p) = u;
+}
+__device__ __forceinline__ void store4_o(f16_t* p, const float* v) {
+  u32x2_t u = {pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])};
   *reinterpret_cast<u32x2_t*>(p) = u;
 }
 
@@ -287,10 +297,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
           u32x4_t pf[QT];
 #pragma unroll
           for (int qt = 0; qt < QT; ++qt)
-            pf[qt] = u32x4_t{pack_bf16x2(s[qt][2 * c][0], s[qt][2 * c][1]),
-                             pack_bf16x2(s[qt][2 * c][2], s[qt][2 * c][3]),
-                             pack_bf16x2(s[qt][2 * c + 1][0], s[qt][2 * c + 1][1]),
-                             pack_bf16x2(s[qt][2 * c + 1][2], s[qt][2 * c + 1][3])};
+            pf[qt] = u32x4_t{pack2<T>(s[qt][2 * c][0], s[qt][2 * c][1]),
+                             pack2<T>(s[qt][2 * c][2], s[qt][2 * c][3]),
+                             pack2<T>(s[qt][2 * c + 1][0], s[qt][2 * c + 1][1]),
+                             pack2<T>(s[qt][2 * c + 1][2], s[qt][2 * c + 1][3])};
 #pragma unroll
           for (int dt = 0; dt < ND; ++dt) {
             const uint8_t* row = sv + (dt * 16 + frow) * VROW;
@@ -677,7 +687,7 @@ static int launch_attn_dma(const void* q, const void* k, const void* v, void* o,
 template <typename T, int HD>
 static int launch_attn(const void* q, const void* k, const void* v, void* o, int B, int H, int Tq,
                        int Tk, const int64_t* st, float scale, int causal, hipStream_t s) {
-  if constexpr (sizeof(T) == 2 && (HD == 64 || HD == 128)) {
+  if constexpr (std::is_same<T, bf16_t>::value && (HD == 64 || HD == 128)) {
     if (attn_dma_ok(Tk, st))
       return launch_attn_dma<HD, 2>(q, k, v, o, B, H, Tq, Tk, st, scale, causal, s);
   }
@@ -731,7 +741,7 @@ extern "C" int cgpt_attention_fwd(const void* q, const void* k, const void* v, v
   if (q == nullptr || k == nullptr || v == nullptr || o == nullptr) return CGPT_EINVAL;
   if (Tk < Tq || Tk == 0) return CGPT_EINVAL;
   if (B * H > 0x7fffffff || Tk > 0x7fffffff) return CGPT_ESHAPE;
-  if (dtype != CGPT_F32 && dtype != CGPT_BF16) return CGPT_EDTYPE;
+  if (dtype != CGPT_F32 && dtype != CGPT_BF16 && dtype != CGPT_F16) return CGPT_EDTYPE;
   const int64_t epc = dtype == CGPT_F32 ? 4 : 8;
   const int64_t st[12] = {q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, o_sb, o_sh, o_st};
   // 16-byte vector loads of Q/K/V rows and 4-element stores of O need every
@@ -750,5 +760,6 @@ extern "C" int cgpt_attention_fwd(const void* q, const void* k, const void* v, v
   const int tq = static_cast<int>(Tq), tk = static_cast<int>(Tk);
   const int hd = static_cast<int>(head_dim);
   if (dtype == CGPT_BF16) return dispatch_hd<bf16_t>(hd, q, k, v, o, b, h, tq, tk, st, scale, causal != 0, s);
+  if (dtype == CGPT_F16) return dispatch_hd<f16_t>(hd, q, k, v, o, b, h, tq, tk, st, scale, causal != 0, s);
   return dispatch_hd<float>(hd, q, k, v, o, b, h, tq, tk, st, scale, causal != 0, s);
 }

@@ -2,13 +2,15 @@
 //
 // Conventions used by every kernel in this directory:
 //  * one wavefront = 64 lanes; blocks are multiples of 64 threads;
-//  * bf16 is stored as raw uint16_t bit patterns and converted with
-//    round-to-nearest-even; arithmetic is always fp32;
+//  * bf16 is stored as raw uint16_t bit patterns, fp16 as _Float16; both are
+//    converted with round-to-nearest-even; arithmetic is always fp32;
 //  * 16-byte vector accesses (dwordx4) for every streaming load/store.
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 #include "../../include/cgpt.h"
 
@@ -40,6 +42,26 @@ __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
   return __builtin_bit_cast(bf16_t, static_cast<__bf16>(f));
 }
 
+// IEEE binary16 (fp16) storage; conversions from fp32 round to nearest even.
+typedef _Float16 f16_t;
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, f16x2_t));
+}
+__device__ __forceinline__ float f16_lo(uint32_t w) {
+  return static_cast<float>(__builtin_bit_cast(f16x2_t, w)[0]);
+}
+__device__ __forceinline__ float f16_hi(uint32_t w) {
+  return static_cast<float>(__builtin_bit_cast(f16x2_t, w)[1]);
+}
+
+// Two fp32 values packed as a pair of 16-bit elements of type T (low half = a).
+template <typename T> __device__ __forceinline__ uint32_t pack2(float a, float b);
+template <> __device__ __forceinline__ uint32_t pack2<bf16_t>(float a, float b) { return pack_bf16x2(a, b); }
+template <> __device__ __forceinline__ uint32_t pack2<f16_t>(float a, float b) { return pack_f16x2(a, b); }
+
 // Element type traits: load/store a float from/to T storage.
 template <typename T> struct Elem;
 template <> struct Elem<float> {
@@ -51,6 +73,11 @@ template <> struct Elem<bf16_t> {
   static constexpr int kVec = 8;
   __device__ static float load(const bf16_t* p) { return bf16_to_f32(*p); }
   __device__ static void store(bf16_t* p, float v) { *p = f32_to_bf16(v); }
+};
+template <> struct Elem<f16_t> {
+  static constexpr int kVec = 8;
+  __device__ static float load(const f16_t* p) { return static_cast<float>(*p); }
+  __device__ static void store(f16_t* p, float v) { *p = static_cast<f16_t>(v); }
 };
 
 // Load/store 16 bytes as kVec floats.
@@ -66,6 +93,14 @@ __device__ __forceinline__ void load_vec(const bf16_t* p, float* out) {
     out[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
   }
 }
+__device__ __forceinline__ void load_vec(const f16_t* p, float* out) {
+  u32x4_t v = *reinterpret_cast<const u32x4_t*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = f16_lo(v[i]);
+    out[2 * i + 1] = f16_hi(v[i]);
+  }
+}
 // The same conversions for 16 bytes already in registers.
 template <typename T> __device__ __forceinline__ void unpack_vec(const u32x4_t& v, float* out);
 template <> __device__ __forceinline__ void unpack_vec<float>(const u32x4_t& v, float* out) {
@@ -79,6 +114,13 @@ template <> __device__ __forceinline__ void unpack_vec<bf16_t>(const u32x4_t& v,
     out[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
   }
 }
+template <> __device__ __forceinline__ void unpack_vec<f16_t>(const u32x4_t& v, float* out) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = f16_lo(v[i]);
+    out[2 * i + 1] = f16_hi(v[i]);
+  }
+}
 __device__ __forceinline__ void store_vec(float* p, const float* in) {
   f32x4_t v = {in[0], in[1], in[2], in[3]};
   *reinterpret_cast<f32x4_t*>(p) = v;
@@ -87,6 +129,12 @@ __device__ __forceinline__ void store_vec(bf16_t* p, const float* in) {
   u32x4_t v;
 #pragma unroll
   for (int i = 0; i < 4; ++i) v[i] = pack_bf16x2(in[2 * i], in[2 * i + 1]);
+  *reinterpret_cast<u32x4_t*>(p) = v;
+}
+__device__ __forceinline__ void store_vec(f16_t* p, const float* in) {
+  u32x4_t v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = pack_f16x2(in[2 * i], in[2 * i + 1]);
   *reinterpret_cast<u32x4_t*>(p) = v;
 }
 
@@ -184,6 +232,12 @@ template <> struct Mfma<bf16_t> {
                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
   }
 };
+template <> struct Mfma<f16_t> {
+  __device__ static void run(const u32x4_t& a, const u32x4_t& b, f32x4_t& c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                               __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+};
 template <> struct Mfma<float> {
   __device__ static void run(const u32x4_t& a, const u32x4_t& b, f32x4_t& c) {
 #pragma unroll
@@ -196,6 +250,10 @@ template <> struct Mfma<float> {
 __device__ __forceinline__ void store4_out(float* p, const float* v) { store_vec(p, v); }
 __device__ __forceinline__ void store4_out(bf16_t* p, const float* v) {
   u32x2_t u = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  *reinterpret_cast<u32x2_t*>(p) = u;
+}
+__device__ __forceinline__ void store4_out(f16_t* p, const float* v) {
+  u32x2_t u = {pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])};
   *reinterpret_cast<u32x2_t*>(p) = u;
 }
 

@@ -11,7 +11,7 @@
 namespace cgpt {
 
 constexpr int kGeluThreads = 256;
-// 16-byte vectors per thread: 16 fp32 or 8 bf16 elements (the fastest of 1, 2,
+// 16-byte vectors per thread: 16 fp32 or 8 bf16 / fp16 elements (the fastest of 1, 2,
 // 4 and 8 per type in a sweep over rotating buffers larger than the MALL).
 template <typename T> constexpr int gelu_unroll() { return sizeof(T) == 4 ? 4 : 1; }
 // Buffer-access cache policy: non-temporal (streamed once, marked for early
@@ -31,7 +31,7 @@ __device__ __forceinline__ u32x4_t gelu_vec16(const u32x4_t& raw) {
     for (int j = 0; j < 4; ++j) out[j] = __float_as_uint(v[j]);
   } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) out[j] = pack_bf16x2(v[2 * j], v[2 * j + 1]);
+    for (int j = 0; j < 4; ++j) out[j] = pack2<T>(v[2 * j], v[2 * j + 1]);
   }
   return out;
 }
@@ -109,5 +109,6 @@ extern "C" int cgpt_gelu(const void* x, void* y, int64_t n, int dtype, void* str
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == CGPT_F32) return launch_gelu<float>(x, y, n, s);
   if (dtype == CGPT_BF16) return launch_gelu<bf16_t>(x, y, n, s);
+  if (dtype == CGPT_F16) return launch_gelu<f16_t>(x, y, n, s);
   return CGPT_EDTYPE;
 }

@@ -49,8 +49,13 @@ __device__ __forceinline__ void buffer_store4(__amdgpu_buffer_rsrc_t r, uint32_t
 }
 #endif
 
-__device__ __forceinline__ float load_bias(const void* bias, bool bf16, int64_t n) {
-  return bf16 ? bf16_to_f32(static_cast<const bf16_t*>(bias)[n]) : static_cast<const float*>(bias)[n];
+// `half`: the bias holds 16-bit elements — fp16 when the inputs are fp16,
+// bf16 otherwise — else fp32.
+template <typename TIn>
+__device__ __forceinline__ float load_bias(const void* bias, bool half, int64_t n) {
+  if (!half) return static_cast<const float*>(bias)[n];
+  if constexpr (std::is_same<TIn, f16_t>::value) return static_cast<float>(static_cast<const f16_t*>(bias)[n]);
+  return bf16_to_f32(static_cast<const bf16_t*>(bias)[n]);
 }
 
 
@@ -85,7 +90,7 @@ __device__ __forceinline__ void store_block_remap(float* scr, TOut* __restrict__
 // Register-staged double-buffered kernel (fp32 and bf16; K % 8 (bf16) or
 // K % 4 (fp32); the K tail of the last 128-byte row is zero-filled).
 
-template <typename TIn, int BM, int BN, int WGM, int WGN, int EPI, typename TOut>
+template <typename TIn, int BM, int BN, int WGM, int WGN, int EPI, typename TOut, bool EL = false>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(
     const TIn* __restrict__ A, const TIn* __restrict__ W, const void* __restrict__ bias,
     bool bias_bf16, TOut* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldw,
@@ -113,6 +118,29 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(
   const int n0 = tile_n * BN;
 
   u32x4_t ra[A_LD], rw[W_LD];
+  // 16 bytes of row `p` from element k: one vector load, or with EL (any K,
+  // stride or alignment) element by element, elements at or past K read as 0.
+  auto chunk = [&](const TIn* p, int k) -> u32x4_t {
+    if constexpr (!EL) {
+      return (k < K) ? *reinterpret_cast<const u32x4_t*>(p + k) : u32x4_t{0, 0, 0, 0};
+    } else {
+      u32x4_t v;
+      if constexpr (sizeof(TIn) == 4) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[e] = k + e < K ? reinterpret_cast<const uint32_t*>(p)[k + e] : 0u;
+      } else {
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t lo = k + 2 * e < K ? h[k + 2 * e] : 0u;
+          const uint32_t hi = k + 2 * e + 1 < K ? h[k + 2 * e + 1] : 0u;
+          v[e] = lo | (hi << 16);
+        }
+      }
+      return v;
+    }
+  };
   // Row indices past the matrix edge are clamped to the last row (the rows are
   // loaded but never stored); the K tail past K is zero-filled.
   auto gload = [&](int kt) {
@@ -122,16 +150,14 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(
       const int q = tid + i * NT;
       const int r = q >> 3, kc = q & 7;
       const int64_t row = min(m0 + r, M - 1);
-      const int k = kbase + kc * EPC;
-      ra[i] = (k < K) ? *reinterpret_cast<const u32x4_t*>(A + row * lda + k) : u32x4_t{0, 0, 0, 0};
+      ra[i] = chunk(A + row * lda, kbase + kc * EPC);
     }
 #pragma unroll
     for (int i = 0; i < W_LD; ++i) {
       const int q = tid + i * NT;
       const int r = q >> 3, kc = q & 7;
       const int64_t row = min(n0 + r, N - 1);
-      const int k = kbase + kc * EPC;
-      rw[i] = (k < K) ? *reinterpret_cast<const u32x4_t*>(W + row * ldw + k) : u32x4_t{0, 0, 0, 0};
+      rw[i] = chunk(W + row * ldw, kbase + kc * EPC);
     }
   };
   auto swrite = [&](int buf) {
@@ -205,7 +231,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         float t = acc[i][j][r];
-        if (EPI != CGPT_EPI_NONE && n + r < N) t += load_bias(bias, bias_bf16, n + r);
+        if (EPI != CGPT_EPI_NONE && n + r < N) t += load_bias<TIn>(bias, bias_bf16, n + r);
         if (EPI == CGPT_EPI_BIAS_GELU) t = gelu_tanh(t);
         if (EPI == CGPT_EPI_BIAS_RESID && n + r < N)
           t += Elem<TOut>::load(C + static_cast<int64_t>(m) * ldc + n + r);
@@ -1264,7 +1290,7 @@ static const TileCfg kF32Tiles[] = {
 constexpr int kNumBf16Tiles = sizeof(kBf16Tiles) / sizeof(kBf16Tiles[0]);
 constexpr int kNumF32Tiles = sizeof(kF32Tiles) / sizeof(kF32Tiles[0]);
 
-template <typename TIn, int BM, int BN, int WGM, int WGN, int EPI, typename TOut>
+template <typename TIn, int BM, int BN, int WGM, int WGN, int EPI, typename TOut, bool EL = false>
 static int launch_cfg(const void* a, const void* w, const void* bias, bool bias_bf16, void* c,
                       int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc, bool vec_store,
                       hipStream_t s) {
@@ -1272,7 +1298,7 @@ static int launch_cfg(const void* a, const void* w, const void* bias, bool bias_
   const int tiles_n = (N + BN - 1) / BN;
   const int64_t blocks = static_cast<int64_t>(tiles_m) * tiles_n;
   if (blocks > 0x7fffffff) return CGPT_ESHAPE;
-  hipLaunchKernelGGL((gemm_kernel<TIn, BM, BN, WGM, WGN, EPI, TOut>), dim3(static_cast<unsigned>(blocks)),
+  hipLaunchKernelGGL((gemm_kernel<TIn, BM, BN, WGM, WGN, EPI, TOut, EL>), dim3(static_cast<unsigned>(blocks)),
                      dim3(64 * WGM * WGN), 0, s, static_cast<const TIn*>(a),
                      static_cast<const TIn*>(w), bias, bias_bf16, static_cast<TOut*>(c), M, N, K,
                      lda, ldw, ldc, tiles_m, tiles_n, vec_store);
@@ -1456,7 +1482,17 @@ static int launch_tile(int tile, const void* a, const void* w, const void* bias,
   case id:                                                                                     \
     return launch_pipe<BM, BN, WGM, WGN, SPS, ST, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, \
                                                              lda, ldw, ldc, vec_store, s);
-  if constexpr (sizeof(TIn) == 2) {
+  if constexpr (std::is_same<TIn, f16_t>::value) {
+    // fp16: the register-staged tiles (the pipelines are bf16 only).
+    switch (tile) {
+      CGPT_GEMM_CASE(0, 256, 256, 2, 2)
+      CGPT_GEMM_CASE(1, 256, 128, 2, 2)
+      CGPT_GEMM_CASE(2, 128, 128, 2, 2)
+      CGPT_GEMM_CASE(3, 128, 64, 2, 2)
+      CGPT_GEMM_CASE(4, 64, 64, 2, 2)
+      default: return CGPT_EINVAL;
+    }
+  } else if constexpr (sizeof(TIn) == 2) {
     switch (tile) {
       CGPT_GEMM_CASE(0, 256, 256, 2, 2)
       CGPT_GEMM_CASE(1, 256, 128, 2, 2)
@@ -1501,7 +1537,8 @@ static int launch_tile(int tile, const void* a, const void* w, const void* bias,
 // Default tile choice when the caller's table has no entry: the register-staged
 // kernel with the largest tile that still gives every CU about two blocks
 // (128x128 for long K, 128x64 otherwise), smaller tiles for small grids.
-static int auto_tile(bool bf16, int M, int N, int K, int64_t lda, int64_t ldw, int epi) {
+static int auto_tile(bool bf16, int M, int N, int K, int64_t lda, int64_t ldw, int epi,
+                     bool pipes = true) {
   // bf16 problems with at least one 256x192 tile per CU: the persistent
   // direct-to-LDS pipelines — 256x256 with wave-staged non-temporal stores
   // for wide N (the LM heads) and for the GELU epilogue; 256x192 with
@@ -1510,7 +1547,7 @@ static int auto_tile(bool bf16, int M, int N, int K, int64_t lda, int64_t ldw, i
   // last round leaves the fewest CUs idle (ties to the larger tile), as long
   // as it still gives half the CUs a tile; below that the register-staged
   // kernel with smaller tiles.
-  if (bf16) {
+  if (bf16 && pipes) {
     auto tiles = [&](int bm, int bn) {
       return static_cast<int64_t>((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     };
@@ -1561,7 +1598,7 @@ static int launch_resid(int req_tile, const void* a, const void* w, const void* 
   constexpr int EPI = CGPT_EPI_BIAS_RESID;
   const int last = sizeof(TIn) == 2 ? kFirstPipeTile - 1 : kNumF32Tiles - 1;
   const bool reg_tile = req_tile >= 0 && req_tile <= last;
-  if constexpr (sizeof(TIn) == 2 && sizeof(TOut) == 4) {
+  if constexpr (std::is_same<TIn, bf16_t>::value && sizeof(TOut) == 4) {
     const int64_t m = M, n = N;
     const int tiles_m = (M + 255) / 256, tiles_n = (N + 191) / 192;
     const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
@@ -1617,7 +1654,23 @@ static int launch_resid(int req_tile, const void* a, const void* w, const void* 
 template <typename TIn, typename TOut>
 static int launch_epi(int epi, int tile, const void* a, const void* w, const void* bias,
                       bool bias_bf16, void* c, int M, int N, int K, int64_t lda, int64_t ldw,
-                      int64_t ldc, bool vec_store, hipStream_t s) {
+                      int64_t ldc, bool vec_store, bool elem_loads, hipStream_t s) {
+  if (elem_loads) {
+    // Any K, stride or alignment: the register-staged 64x64 tile with element
+    // loads, every epilogue (the residual one included).
+#define CGPT_EL_CASE(E)                                                                         \
+  case E:                                                                                       \
+    return launch_cfg<TIn, 64, 64, 2, 2, E, TOut, true>(a, w, bias, bias_bf16, c, M, N, K, lda, \
+                                                        ldw, ldc, vec_store, s);
+    switch (epi) {
+      CGPT_EL_CASE(CGPT_EPI_NONE)
+      CGPT_EL_CASE(CGPT_EPI_BIAS)
+      CGPT_EL_CASE(CGPT_EPI_BIAS_GELU)
+      CGPT_EL_CASE(CGPT_EPI_BIAS_RESID)
+      default: return CGPT_EINVAL;
+    }
+#undef CGPT_EL_CASE
+  }
   switch (epi) {
     case CGPT_EPI_BIAS_RESID:
       return launch_resid<TIn, TOut>(tile, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc,
@@ -1641,8 +1694,8 @@ namespace cgpt {
 // Argument checks shared by the GEMM entry points: CGPT_OK when the problem is
 // well formed (M == 0 or N == 0 included: nothing to launch).
 int validate_gemm(const void* a, const void* w, const void* bias, const void* c, int64_t M,
-                         int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldc, int in_dtype,
-                         int bias_dtype, int out_dtype, int epilogue) {
+                  int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldc, int in_dtype,
+                  int bias_dtype, int out_dtype, int epilogue, bool* elem_loads) {
   if (M < 0 || N < 0 || K < 0) return CGPT_EINVAL;
   if (M == 0 || N == 0) return CGPT_OK;
   if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff) return CGPT_ESHAPE;
@@ -1651,17 +1704,33 @@ int validate_gemm(const void* a, const void* w, const void* bias, const void* c,
       epilogue != CGPT_EPI_BIAS_RESID)
     return CGPT_EINVAL;
   if (epilogue != CGPT_EPI_NONE && bias == nullptr) return CGPT_EINVAL;
-  if (in_dtype != CGPT_F32 && in_dtype != CGPT_BF16) return CGPT_EDTYPE;
-  if (out_dtype != CGPT_F32 && out_dtype != CGPT_BF16) return CGPT_EDTYPE;
-  if (epilogue != CGPT_EPI_NONE && bias_dtype != CGPT_F32 && bias_dtype != CGPT_BF16)
+  const bool f16 = in_dtype == CGPT_F16 && elem_loads != nullptr;
+  if (in_dtype != CGPT_F32 && in_dtype != CGPT_BF16 && !f16) return CGPT_EDTYPE;
+  // Outputs and bias: fp32, or the 16-bit type of the inputs' family (fp16
+  // with fp16 inputs, bf16 otherwise).
+  const int half = f16 ? CGPT_F16 : CGPT_BF16;
+  if (out_dtype != CGPT_F32 && out_dtype != half) return CGPT_EDTYPE;
+  if (epilogue != CGPT_EPI_NONE && bias_dtype != CGPT_F32 && bias_dtype != half)
     return CGPT_EDTYPE;
-  const int64_t epc = in_dtype == CGPT_BF16 ? 8 : 4;
-  if (K == 0 || K % epc != 0) return CGPT_ESHAPE;
+  if (K == 0) return CGPT_ESHAPE;
   if (lda < K || ldw < K || ldc < N) return CGPT_EINVAL;
+  const int64_t epc = in_dtype == CGPT_F32 ? 4 : 8;
+  const int64_t ealign = in_dtype == CGPT_F32 ? 4 : 2;
+  const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pw = reinterpret_cast<uintptr_t>(w);
+  const uintptr_t pb = epilogue != CGPT_EPI_NONE ? reinterpret_cast<uintptr_t>(bias) : 0;
+  if (elem_loads != nullptr) {
+    // Element alignment is all the element-load kernel needs.
+    if (pa % ealign != 0 || pw % ealign != 0 ||
+        pb % (bias_dtype == CGPT_F32 ? 4 : 2) != 0 ||
+        reinterpret_cast<uintptr_t>(c) % (out_dtype == CGPT_F32 ? 4 : 2) != 0)
+      return CGPT_EINVAL;
+    *elem_loads = K % epc != 0 || lda % epc != 0 || ldw % epc != 0 || (pa & 15) || (pw & 15) ||
+                  (pb & 15);
+    return CGPT_OK;
+  }
+  if (K % epc != 0) return CGPT_ESHAPE;
   if (lda % epc != 0 || ldw % epc != 0) return CGPT_EINVAL;
-  if ((reinterpret_cast<uintptr_t>(a) & 15) || (reinterpret_cast<uintptr_t>(w) & 15))
-    return CGPT_EINVAL;
-  if (epilogue != CGPT_EPI_NONE && (reinterpret_cast<uintptr_t>(bias) & 15)) return CGPT_EINVAL;
+  if ((pa & 15) || (pw & 15) || (pb & 15)) return CGPT_EINVAL;
   return CGPT_OK;
 }
 }  // namespace cgpt
@@ -1723,55 +1792,66 @@ extern "C" int cgpt_gemm(const void* a, const void* w, const void* bias, void* c
                          int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldc, int in_dtype,
                          int bias_dtype, int out_dtype, int epilogue, int tile, void* stream) {
   using namespace cgpt;
+  bool el = false;
   const int st = validate_gemm(a, w, bias, c, M, N, K, lda, ldw, ldc, in_dtype, bias_dtype,
-                               out_dtype, epilogue);
+                               out_dtype, epilogue, &el);
   if (st != CGPT_OK || M == 0 || N == 0) return st;
-  const bool bf16 = in_dtype == CGPT_BF16;
-  const int nt = bf16 ? kNumBf16Tiles : kNumF32Tiles;
+  const bool bf16 = in_dtype == CGPT_BF16, f16 = in_dtype == CGPT_F16;
+  const int nt = bf16 ? kNumBf16Tiles : f16 ? kFirstPipeTile : kNumF32Tiles;
+  const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool bb = bias_dtype != CGPT_F32;
+  const bool out16 = out_dtype != CGPT_F32;
+  const int64_t out_align = out16 ? 8 : 16;
+  const bool vec_store = (ldc % 4 == 0) && (reinterpret_cast<uintptr_t>(c) % out_align == 0);
+  if (tile == CGPT_TILE_SKINNY && (el || f16)) return CGPT_EINVAL;  // vector-rule bf16 / fp32 only
+  if (tile != CGPT_TILE_AUTO && tile != CGPT_TILE_SKINNY && (tile < 0 || tile >= nt))
+    return CGPT_EINVAL;
   if (epilogue == CGPT_EPI_BIAS_RESID) {
     if (tile == CGPT_TILE_SKINNY) return CGPT_EINVAL;  // not a skinny epilogue
-    if (tile != CGPT_TILE_AUTO && (tile < 0 || tile >= nt)) return CGPT_EINVAL;
     // launch_resid picks the kernel (tile: a preference).
-    const int64_t out_align = out_dtype == CGPT_F32 ? 16 : 8;
-    const bool vec_store = (ldc % 4 == 0) && (reinterpret_cast<uintptr_t>(c) % out_align == 0);
-    const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const bool bb = bias_dtype == CGPT_BF16;
-    if (bf16 && out_dtype == CGPT_BF16)
+    if (el) {
+      if (f16)
+        return out16 ? launch_epi<f16_t, f16_t>(epilogue, 0, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, true, s)
+                     : launch_epi<f16_t, float>(epilogue, 0, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, true, s);
+      if (bf16)
+        return out16 ? launch_epi<bf16_t, bf16_t>(epilogue, 0, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, true, s)
+                     : launch_epi<bf16_t, float>(epilogue, 0, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, true, s);
+      return out16 ? launch_epi<float, bf16_t>(epilogue, 0, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, true, s)
+                   : launch_epi<float, float>(epilogue, 0, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, true, s);
+    }
+    if (f16)
+      return out16 ? launch_resid<f16_t, f16_t>(tile, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, s)
+                   : launch_resid<f16_t, float>(tile, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, s);
+    if (bf16 && out16)
       return launch_resid<bf16_t, bf16_t>(tile, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, s);
     if (bf16)
       return launch_resid<bf16_t, float>(tile, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, s);
-    if (out_dtype == CGPT_F32)
+    if (!out16)
       return launch_resid<float, float>(tile, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, s);
     return launch_resid<float, bf16_t>(tile, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, s);
   }
-  if (tile == CGPT_TILE_AUTO && M <= 64) tile = CGPT_TILE_SKINNY;
+  if (tile == CGPT_TILE_AUTO && M <= 64 && !el && !f16) tile = CGPT_TILE_SKINNY;
   if (tile == CGPT_TILE_SKINNY) {
     if (M > 64) return CGPT_ESHAPE;
-    return launch_gemm_skinny(bf16, epilogue, a, w, bias, bias_dtype == CGPT_BF16, c,
-                              out_dtype == CGPT_BF16, static_cast<int>(M), static_cast<int>(N),
-                              static_cast<int>(K), lda, ldw, ldc, nullptr, 0, nullptr, 0,
-                              static_cast<hipStream_t>(stream));
+    return launch_gemm_skinny(bf16, epilogue, a, w, bias, bb, c, out16, m, n, k, lda, ldw, ldc,
+                              nullptr, 0, nullptr, 0, s);
   }
-  if (tile == CGPT_TILE_AUTO)
-    tile = auto_tile(bf16, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), lda, ldw,
-                     epilogue);
-  if (tile < 0 || tile >= nt) return CGPT_EINVAL;
+  if (el) tile = 0;  // the element-load kernel has one tile
+  if (tile == CGPT_TILE_AUTO) tile = auto_tile(bf16 || f16, m, n, k, lda, ldw, epilogue, !f16);
   if (bf16 && tile >= kFirstPipeTile && !pipe_ok(tile, M, N, K, lda, ldw)) return CGPT_ESHAPE;
-  const int64_t out_align = out_dtype == CGPT_F32 ? 16 : 8;
-  const bool vec_store = (ldc % 4 == 0) && (reinterpret_cast<uintptr_t>(c) % out_align == 0);
-  const bool bias_bf16 = bias_dtype == CGPT_BF16;
-  hipStream_t s = static_cast<hipStream_t>(stream);
   if (bf16 && tile >= kFirstPipeTile) {
     const int pst = maybe_prefetch_w(w, M, N, K, ldw, s);
     if (pst != CGPT_OK) return pst;
   }
-  const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
-  if (bf16 && out_dtype == CGPT_BF16)
-    return launch_epi<bf16_t, bf16_t>(epilogue, tile, a, w, bias, bias_bf16, c, m, n, k, lda, ldw, ldc, vec_store, s);
+  if (f16)
+    return out16 ? launch_epi<f16_t, f16_t>(epilogue, tile, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, el, s)
+                 : launch_epi<f16_t, float>(epilogue, tile, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, el, s);
+  if (bf16 && out16)
+    return launch_epi<bf16_t, bf16_t>(epilogue, tile, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, el, s);
   if (bf16)
-    return launch_epi<bf16_t, float>(epilogue, tile, a, w, bias, bias_bf16, c, m, n, k, lda, ldw, ldc, vec_store, s);
-  if (out_dtype == CGPT_F32)
-    return launch_epi<float, float>(epilogue, tile, a, w, bias, bias_bf16, c, m, n, k, lda, ldw, ldc, vec_store, s);
-  return launch_epi<float, bf16_t>(epilogue, tile, a, w, bias, bias_bf16, c, m, n, k, lda, ldw, ldc, vec_store, s);
+    return launch_epi<bf16_t, float>(epilogue, tile, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, el, s);
+  if (!out16)
+    return launch_epi<float, float>(epilogue, tile, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, el, s);
+  return launch_epi<float, bf16_t>(epilogue, tile, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, el, s);
 }

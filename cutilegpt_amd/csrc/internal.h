@@ -8,10 +8,15 @@ namespace cgpt {
 
 // Argument checks shared by the GEMM entry points (cgpt_gemm, the skinny
 // variants): CGPT_OK when the problem is well formed, M == 0 or N == 0
-// included (nothing to launch).
+// included (nothing to launch).  Without `elem_loads` (the skinny kernels)
+// inputs are fp32 or bf16 and must follow the 16-byte vector rules (K, lda
+// and ldw multiples of the elements in 16 bytes, A, W and bias 16-byte
+// aligned).  With it (cgpt_gemm) fp16 inputs are accepted too, and
+// *elem_loads tells whether the problem breaks those rules and needs the
+// element-load kernel.
 int validate_gemm(const void* a, const void* w, const void* bias, const void* c, int64_t M,
                   int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldc, int in_dtype,
-                  int bias_dtype, int out_dtype, int epilogue);
+                  int bias_dtype, int out_dtype, int epilogue, bool* elem_loads = nullptr);
 
 // Skinny GEMM (M <= 64): C[M,N] = epilogue(A W^T + bias).  Column slices of
 // C, K split across the block's waves and (when workspace and counters are

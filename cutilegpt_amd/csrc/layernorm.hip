@@ -589,9 +589,71 @@ static int launch_lnp(const float* x, const float* parts, int n, int ps, int ldp
   return hip_status(hipGetLastError());
 }
 
+// ---- any width, any element alignment, every dtype combination
+//
+// One 256-thread block per row; thread t owns columns t, t + 256, ...  Three
+// passes over the row: the sum of x (+ delta), the centred sum of squares,
+// then x_out and y — the second and third re-read the row (from L2 for rows
+// up to a few MB).  Dtypes are launch arguments (uniform branches).  Used for
+// what the vector kernels above do not take: fp16, widths not a multiple of
+// 4 or above 4096, rows that are not 16-byte (fp32) / 8-byte aligned.  Same
+// arithmetic as those kernels (fp32 sums, mean and centred variance divided
+// by cols, y = (v - mean) * rstd * gamma + beta) up to summation order.
+__device__ __forceinline__ float ld_any(const void* p, int dt, int64_t i) {
+  if (dt == CGPT_F32) return static_cast<const float*>(p)[i];
+  if (dt == CGPT_BF16) return bf16_to_f32(static_cast<const bf16_t*>(p)[i]);
+  return static_cast<float>(static_cast<const f16_t*>(p)[i]);
+}
+__device__ __forceinline__ void st_any(void* p, int dt, int64_t i, float v) {
+  if (dt == CGPT_F32) static_cast<float*>(p)[i] = v;
+  else if (dt == CGPT_BF16) static_cast<bf16_t*>(p)[i] = f32_to_bf16(v);
+  else static_cast<f16_t*>(p)[i] = static_cast<f16_t>(v);
+}
+
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+  v = wave_sum(v);
+  const int wave = threadIdx.x >> 6;
+  __syncthreads();  // earlier readers of red are done
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+__global__ __launch_bounds__(kLnThreads) void add_layernorm_any_kernel(
+    const void* x, const void* delta, void* x_out, const void* gamma, const void* beta, void* y,
+    int64_t cols, float eps, int xd, int dd, int pd, int yd) {
+  __shared__ float red[kLnThreads / 64];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * cols;
+  auto val = [&](int64_t c) {
+    const float v = ld_any(x, xd, base + c);
+    return delta != nullptr ? v + ld_any(delta, dd, base + c) : v;
+  };
+  const float n_f = static_cast<float>(cols);
+  float sum = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += kLnThreads) sum += val(c);
+  const float mean = block_sum256(sum, red) / n_f;
+  float sq = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += kLnThreads) {
+    const float t = val(c) - mean;
+    sq += t * t;
+  }
+  const float rstd = 1.0f / sqrtf(block_sum256(sq, red) / n_f + eps);
+  // Every element is read and then written by the same thread, so x_out or y
+  // may alias x.
+  for (int64_t c = threadIdx.x; c < cols; c += kLnThreads) {
+    const float v = val(c);
+    if (x_out != nullptr) st_any(x_out, xd, base + c, v);
+    st_any(y, yd, base + c, (v - mean) * rstd * ld_any(gamma, pd, c) + ld_any(beta, pd, c));
+  }
+}
+
 static bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7) == 0; }
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 static bool dtype_ok(int d) { return d == CGPT_F32 || d == CGPT_BF16; }
+static bool dtype_any_ok(int d) { return d == CGPT_F32 || d == CGPT_BF16 || d == CGPT_F16; }
+static bool elem_aligned(const void* p, int dtype) {
+  return (reinterpret_cast<uintptr_t>(p) & (dtype == CGPT_F32 ? 3 : 1)) == 0;
+}
 static bool ptr_aligned(const void* p, int dtype) {
   return p == nullptr || (dtype == CGPT_F32 ? aligned16(p) : aligned8(p));
 }
@@ -606,17 +668,30 @@ extern "C" int cgpt_add_layernorm(const void* x, const void* delta, void* x_out,
   if (rows < 0 || cols <= 0) return CGPT_EINVAL;
   if (rows == 0) return CGPT_OK;
   if (x == nullptr || gamma == nullptr || beta == nullptr || y == nullptr) return CGPT_EINVAL;
-  if (!dtype_ok(x_dtype) || !dtype_ok(param_dtype) || !dtype_ok(y_dtype) ||
-      (delta != nullptr && !dtype_ok(delta_dtype)))
+  if (!dtype_any_ok(x_dtype) || !dtype_any_ok(param_dtype) || !dtype_any_ok(y_dtype) ||
+      (delta != nullptr && !dtype_any_ok(delta_dtype)))
     return CGPT_EDTYPE;
-  // Four-element vectors per lane: rows must keep 4-element alignment.
-  if (cols % 4 != 0 || cols > 4096) return CGPT_ESHAPE;
-  if (!ptr_aligned(x, x_dtype) || !ptr_aligned(x_out, x_dtype) || !ptr_aligned(y, y_dtype) ||
-      !ptr_aligned(gamma, param_dtype) || !ptr_aligned(beta, param_dtype) ||
-      (delta != nullptr && !ptr_aligned(delta, delta_dtype)))
+  if (!elem_aligned(x, x_dtype) || (x_out != nullptr && !elem_aligned(x_out, x_dtype)) ||
+      !elem_aligned(y, y_dtype) || !elem_aligned(gamma, param_dtype) ||
+      !elem_aligned(beta, param_dtype) || (delta != nullptr && !elem_aligned(delta, delta_dtype)))
     return CGPT_EINVAL;
   if (!(eps >= 0.f)) return CGPT_EINVAL;
+  if (cols > 0x7fffffff) return CGPT_ESHAPE;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // The vector kernels: fp32 / bf16, four-element vectors per lane (rows
+  // keep 4-element alignment), whole rows in registers up to 4096 columns.
+  const bool vec = dtype_ok(x_dtype) && dtype_ok(param_dtype) && dtype_ok(y_dtype) &&
+                   (delta == nullptr || dtype_ok(delta_dtype)) && cols % 4 == 0 && cols <= 4096 &&
+                   ptr_aligned(x, x_dtype) && ptr_aligned(x_out, x_dtype) &&
+                   ptr_aligned(y, y_dtype) && ptr_aligned(gamma, param_dtype) &&
+                   ptr_aligned(beta, param_dtype) && (delta == nullptr || ptr_aligned(delta, delta_dtype));
+  if (!vec) {
+    if (rows > 0x7fffffff) return CGPT_ESHAPE;
+    hipLaunchKernelGGL(add_layernorm_any_kernel, dim3(static_cast<unsigned>(rows)), dim3(kLnThreads),
+                       0, s, x, delta, x_out, gamma, beta, y, cols, eps, x_dtype, delta_dtype,
+                       param_dtype, y_dtype);
+    return hip_status(hipGetLastError());
+  }
   const bool pb = param_dtype == CGPT_BF16;
   const int c = static_cast<int>(cols);
   if (x_dtype == CGPT_BF16 && y_dtype == CGPT_BF16 && pb && delta == nullptr &&

@@ -6,7 +6,8 @@ the hand-written gfx950 kernels of ``libcgpt.so`` on
 ``torch.cuda.current_stream()``, returns a freshly allocated output and never
 mutates its inputs.  Tensors must live on the GPU; anything else raises
 ``ValueError`` (the reference raises ``ValueError`` for non-device arrays, e.g.
-``cutile_gpt/kernels/gelu.py:81-82``).  Supported dtypes: float32, bfloat16.
+``cutile_gpt/kernels/gelu.py:81-82``).  Supported dtypes: float32, bfloat16 and
+float16 (the reference's wrappers take float32 and float16).
 
 The fused entry points (``add_layer_norm``, ``linear_bias_gelu``,
 ``attention_qkv``, ``token_pos_embedding``) are what ``CutileGPT.forward`` uses;
@@ -24,14 +25,16 @@ import torch
 from . import _lib
 from .tiles import gemm_tile
 
-_DT = {torch.float32: _lib.CGPT_F32, torch.bfloat16: _lib.CGPT_BF16}
+_DT = {torch.float32: _lib.CGPT_F32, torch.bfloat16: _lib.CGPT_BF16,
+       torch.float16: _lib.CGPT_F16}
 
 
 def _dtype_code(t: torch.Tensor, name: str) -> int:
     try:
         return _DT[t.dtype]
     except KeyError:
-        raise ValueError(f"{name}: unsupported dtype {t.dtype} (float32 or bfloat16)") from None
+        raise ValueError(f"{name}: unsupported dtype {t.dtype} "
+                         "(float32, bfloat16 or float16)") from None
 
 
 def _require_gpu(name: str, *tensors: Optional[torch.Tensor]) -> None:
@@ -118,9 +121,10 @@ def cutile_layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor,
                       eps: float = 1e-5) -> torch.Tensor:
     """LayerNorm over the last axis (biased variance), output in ``x.dtype``.
 
-    Replaces ``cutile_layer_norm`` (``cutile_gpt/kernels/layernorm.py:77-135``);
-    rows of any width up to 4096 (multiple of 4) run without the reference's
-    power-of-two padding copies.
+    Replaces ``cutile_layer_norm`` (``cutile_gpt/kernels/layernorm.py:77-135``)
+    for rows of any width, without the reference's power-of-two padding copies:
+    float32 / bfloat16 rows of a multiple of 4 up to 4096 elements stay in
+    registers, other widths and float16 take a block-per-row kernel.
     """
     return add_layer_norm(x, None, weight, bias, eps)
 
@@ -211,13 +215,19 @@ def _attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tenso
         *qs, *ks, *vs, *os_, float(scale), int(causal), _dtype_code(q, name), _stream()), name)
 
 
+_ATTN_HD = (16, 32, 64, 128)  # head_dim values the attention kernels are built for
+
+
 def cutile_causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                             n_head: int) -> torch.Tensor:
     """Causal softmax attention on (batch, n_head, seq_len, head_dim) tensors.
 
     Replaces ``cutile_causal_attention`` (``cutile_gpt/kernels/attention.py:119-175``).
     Inputs may be any strided views whose last axis is contiguous (no copies);
-    head_dim in {16, 32, 64, 128}; the output is a new contiguous tensor.
+    the output is a new contiguous tensor.  The kernels take head_dim 16, 32, 64
+    or 128; other head_dim up to 128 are zero-padded to the next of those (the
+    padded columns add 0 to every score and give output columns that are
+    dropped; the scale stays 1/sqrt(head_dim)).
     """
     _require_gpu("cutile_causal_attention", q, k, v)
     if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
@@ -225,6 +235,17 @@ def cutile_causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if not (q.dtype == k.dtype == v.dtype):
         raise ValueError("cutile_causal_attention: q, k, v dtypes differ")
     B, H, T, hd = q.shape
+    hp = next((d for d in _ATTN_HD if d >= hd), None)
+    if hd < 1 or hp is None:
+        raise ValueError(f"cutile_causal_attention: head_dim {hd} outside 1..{_ATTN_HD[-1]}")
+    if hp != hd:
+        pad = lambda t: torch.nn.functional.pad(t, (0, hp - hd))
+        o = torch.empty((B, H, T, hp), dtype=q.dtype, device=q.device)
+        qp, kp, vp = pad(q), pad(k), pad(v)
+        _attention(qp, kp, vp, o, B, H, T, T, hp, qp.stride()[:3], kp.stride()[:3],
+                   vp.stride()[:3], o.stride()[:3], 1.0 / math.sqrt(hd), True,
+                   "cutile_causal_attention")
+        return o[..., :hd].contiguous()
 
     def fix(t):
         if t.stride(-1) != 1 or t.data_ptr() % 16 or any(s % 8 for s in t.stride()[:3]):

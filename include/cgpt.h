@@ -13,8 +13,10 @@
  *   - has no mutable global state, so concurrent calls on different streams
  *     are safe.
  *
- * Element types are CGPT_F32 (IEEE fp32) and CGPT_BF16 (bfloat16 bit
- * patterns); all arithmetic is fp32, bf16 outputs are rounded to nearest even.
+ * Element types are CGPT_F32 (IEEE fp32), CGPT_BF16 (bfloat16 bit patterns)
+ * and CGPT_F16 (IEEE binary16; the GEMM, LayerNorm, GELU, attention and
+ * embedding entry points); all arithmetic is fp32, 16-bit outputs are rounded
+ * to nearest even.
  *
  * Reference citations are relative to the falcons-eyes/cutileGPT checkout.
  */
@@ -39,6 +41,7 @@ extern "C" {
 /* element types */
 #define CGPT_F32 0
 #define CGPT_BF16 1
+#define CGPT_F16 2
 
 /* GEMM epilogues */
 #define CGPT_EPI_NONE 0        /* C = A W^T                                  */
@@ -66,6 +69,10 @@ int cgpt_gelu(const void* x, void* y, int64_t n, int dtype, void* stream);
  *   y     = (s - mean(s)) / sqrt(var(s) + eps) * gamma + beta   (biased var)
  * Row r of x / delta / x_out / y starts at r * cols.  gamma and beta hold
  * `cols` elements of `param_dtype`.  Statistics are accumulated in fp32.
+ * Any cols >= 1 and any dtype mix of CGPT_F32 / CGPT_BF16 / CGPT_F16 with
+ * element-aligned pointers: fp32 / bf16 rows of cols % 4 == 0, cols <= 4096,
+ * 16-byte (fp32) or 8-byte (bf16) aligned take the register-resident vector
+ * kernels, the rest a block-per-row kernel (three passes over the row).
  * Replaces cutile_layer_norm, cutile_gpt/kernels/layernorm.py:77-135 (kernel
  * :24-74), fused with the residual adds at cutile_gpt/models/gpt.py:155,174.
  */
@@ -98,13 +105,20 @@ int cgpt_add_layernorm_partials(const void* x, const float* partials, int64_t n_
  * A row-major with leading dimension lda, W row-major (out_features, in_features)
  * with leading dimension ldw — the nn.Linear / cutileGPT `weight` layout, so no
  * transposed copy is needed — C row-major with leading dimension ldc.
- * in_dtype is the type of A and W (both CGPT_BF16 -> bf16 MFMA, both CGPT_F32 ->
- * fp32 MFMA); accumulation is fp32; bias (bias_dtype) is added in fp32; C is
- * written as out_dtype.  Requires K % 8 == 0 (bf16) or K % 4 == 0 (fp32), lda /
- * ldw multiples of 8 (bf16) or 4 (fp32) elements and 16-byte aligned A, W and bias.
+ * in_dtype is the type of A and W (CGPT_BF16 -> bf16 MFMA, CGPT_F16 -> fp16
+ * MFMA, CGPT_F32 -> fp32 MFMA); accumulation is fp32; bias (bias_dtype) is
+ * added in fp32; C is written as out_dtype.  bias_dtype and out_dtype are
+ * CGPT_F32 or the 16-bit type of the inputs' family (CGPT_F16 with fp16 inputs,
+ * CGPT_BF16 otherwise).  Any K >= 1, lda >= K, ldw >= K and element-aligned
+ * pointers: problems with K, lda and ldw multiples of 8 (16-bit) or 4 (fp32)
+ * elements and 16-byte aligned A, W and bias take the vector kernels below;
+ * others run a 64x64 register-staged kernel that loads element by element
+ * (any tile id but CGPT_TILE_SKINNY is then ignored).  fp16 runs the
+ * register-staged tiles 0-4 only.
  * `tile` selects a tile configuration: CGPT_TILE_AUTO = library heuristic (the
- * skinny kernel when M <= 64); CGPT_TILE_SKINNY = the weight-streaming kernel
- * for M <= 64 rows (decode steps: one row per sequence), CGPT_ESHAPE above.
+ * skinny kernel when M <= 64, fp32 / bf16); CGPT_TILE_SKINNY = the
+ * weight-streaming kernel for M <= 64 rows (decode steps: one row per
+ * sequence), CGPT_ESHAPE above; fp32 and bf16 under the vector rules only.
  * With CGPT_EPI_BIAS_RESID (C += A W^T + bias in place, C usually the fp32
  * residual stream), tile 14 asks for the slab kernel's residual ring, a
  * register-staged id (bf16 0-4, fp32 0-1) for that tile, and any other id
@@ -216,7 +230,11 @@ int cgpt_attention_fwd(const void* q, const void* k, const void* v, void* o,
  * for i < n_tokens; idx holds int64 token ids; wpe may be NULL (plain gather).
  * Ids outside [0, vocab) or positions outside [0, n_pos) are clamped into range
  * (so the kernel never reads out of bounds) and, when err_flag is not NULL,
- * set *err_flag (a device int) to 1.
+ * set *err_flag (a device int) to 1.  Any D >= 1 with element-aligned
+ * pointers (four-element vectors when D % 4 == 0 and rows are 16-byte (fp32) /
+ * 8-byte (16-bit) aligned, else element by element); w_dtype CGPT_F32 or
+ * CGPT_BF16 with out_dtype CGPT_F32 or CGPT_BF16, or CGPT_F16 with CGPT_F16 /
+ * CGPT_F32.
  * Replaces cutile_embedding, cutile_gpt/kernels/embedding.py:54-109 (kernel
  * :23-51), fused with the token+position add at cutile_gpt/models/gpt.py:110-113.
  */

@@ -42,19 +42,23 @@ def test_abi_rejects_bad_arguments_before_launch():
     from cutilegpt_amd import _lib
     lib = _lib.load()
     fake = 1 << 20  # 16-byte aligned, never dereferenced
-    # gemm: K not a multiple of 8 for bf16, bad epilogue, missing bias, misaligned A, bad dtype
-    assert lib.cgpt_gemm(fake, fake, None, fake, 4, 4, 12, 12, 12, 4, 1, 1, 1, 0, -1, None) == -3
+    # gemm: A not element-aligned (any K is accepted), bad epilogue, missing bias, bad dtype,
+    # fp16 inputs with a bf16 bias / output, lda < K, unknown tile
+    assert lib.cgpt_gemm(fake + 1, fake, None, fake, 4, 4, 12, 12, 12, 4, 1, 1, 1, 0, -1, None) == -1
+    assert lib.cgpt_gemm(fake, fake, fake, fake, 4, 4, 16, 16, 16, 4, 2, 1, 2, 1, -1, None) == -2
+    assert lib.cgpt_gemm(fake, fake, None, fake, 4, 4, 16, 16, 16, 4, 2, 2, 1, 0, -1, None) == -2
     assert lib.cgpt_gemm(fake, fake, None, fake, 4, 4, 16, 16, 16, 4, 1, 1, 1, 7, -1, None) == -1
     assert lib.cgpt_gemm(fake, fake, None, fake, 4, 4, 16, 16, 16, 4, 1, 1, 1, 1, -1, None) == -1
-    assert lib.cgpt_gemm(fake + 2, fake, None, fake, 4, 4, 16, 16, 16, 4, 1, 1, 1, 0, -1, None) == -1
+    assert lib.cgpt_gemm(fake, fake + 3, None, fake, 4, 4, 16, 16, 16, 4, 0, 0, 0, 0, -1, None) == -1
     assert lib.cgpt_gemm(fake, fake, None, fake, 4, 4, 16, 16, 16, 4, 5, 1, 1, 0, -1, None) == -2
     assert lib.cgpt_gemm(fake, fake, None, fake, 4, 4, 16, 8, 16, 4, 1, 1, 1, 0, -1, None) == -1
     assert lib.cgpt_gemm(fake, fake, None, fake, 4, 4, 16, 16, 16, 4, 1, 1, 1, 0, 99, None) == -1
     # empty problems are a no-op success
     assert lib.cgpt_gemm(None, None, None, None, 0, 4, 16, 16, 16, 4, 1, 1, 1, 0, -1, None) == 0
-    # layernorm: cols not multiple of 4 / too wide / bad dtype / null gamma
-    assert lib.cgpt_add_layernorm(fake, None, None, fake, fake, fake, 2, 6, 1e-5, 0, 0, 0, 0, None) == -3
-    assert lib.cgpt_add_layernorm(fake, None, None, fake, fake, fake, 2, 8192, 1e-5, 0, 0, 0, 0, None) == -3
+    # layernorm (any width): x / y not element-aligned, bad dtype, null gamma, negative eps
+    assert lib.cgpt_add_layernorm(fake + 2, None, None, fake, fake, fake, 2, 6, 1e-5, 0, 0, 0, 0, None) == -1
+    assert lib.cgpt_add_layernorm(fake, None, None, fake, fake, fake + 1, 2, 6, 1e-5, 2, 0, 2, 2, None) == -1
+    assert lib.cgpt_add_layernorm(fake, None, None, fake, fake, fake, 2, 8192, -1.0, 0, 0, 0, 0, None) == -1
     assert lib.cgpt_add_layernorm(fake, None, None, fake, fake, fake, 2, 8, 1e-5, 3, 0, 0, 0, None) == -2
     assert lib.cgpt_add_layernorm(fake, None, None, None, fake, fake, 2, 8, 1e-5, 0, 0, 0, 0, None) == -1
     # attention: unsupported head_dim, Tk < Tq, unaligned strides, bad scale
@@ -67,7 +71,9 @@ def test_abi_rejects_bad_arguments_before_launch():
     # gelu / embedding
     assert lib.cgpt_gelu(fake, fake, 10, 9, None) == -2
     assert lib.cgpt_gelu(None, None, 0, 0, None) == 0
-    assert lib.cgpt_embedding(fake, fake, None, fake, 4, 4, 6, 10, 0, 0, 0, 0, None, None) == -3
+    # embedding (any width): wte not element-aligned, fp16 weights into bf16
+    assert lib.cgpt_embedding(fake, fake + 2, None, fake, 4, 4, 6, 10, 0, 0, 0, 0, None, None) == -1
+    assert lib.cgpt_embedding(fake, fake, None, fake, 4, 4, 6, 10, 0, 0, 2, 1, None, None) == -2
     # embedding + LayerNorm: D not a multiple of 4, missing wpe, bad dtype, misaligned x_out
     el = lambda wpe, x, D, wd: lib.cgpt_embedding_layernorm(fake, fake, wpe, None, x, fake, fake, fake,
                                                              4, 4, D, 10, 0, 8, 1e-5, wd, 0, None, None)

@@ -387,7 +387,7 @@ def test_attention_qkv_rejects_bad_arguments(gpu):
     with pytest.raises(ValueError):
         cg.attention_qkv(x.cpu(), 2)
     with pytest.raises(ValueError):
-        cg.attention_qkv(x.half(), 2)
+        cg.attention_qkv(x.double(), 2)  # float64 is not a kernel dtype
 
 
 def test_attention_qkv_strided_view(gpu):
