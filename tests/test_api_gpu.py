@@ -28,7 +28,7 @@ def lin(x, w, b=None):
     return y if b is None else y + b.double()
 
 
-@pytest.mark.parametrize("dtype", [F32, BF16])
+@pytest.mark.parametrize("dtype", [F32, BF16, torch.float16])
 def test_linear_gelu_chain_fused_and_unfused(gpu, dtype):
     x = randn(2, 40, 64, seed=1, dtype=dtype)
     w = randn(192, 64, seed=2, scale=0.1, dtype=dtype)
@@ -38,7 +38,7 @@ def test_linear_gelu_chain_fused_and_unfused(gpu, dtype):
     fused = op.execute()
     plain = op.execute(optimize=False)
     assert fused.shape == plain.shape == (2, 40, 192)
-    tol = 1e-5 if dtype == F32 else 3e-2
+    tol = {F32: 1e-5, BF16: 3e-2, torch.float16: 4e-3}[dtype]
     assert max_err(fused, ref) < tol
     assert max_err(plain, ref) < tol
 
@@ -61,6 +61,21 @@ def test_explicit_tile_configs_agree(gpu, cfg):
     assert op.ops[-1].tile_config.gemm_tile(BF16) is not None
     out = op.execute()
     assert max_err(out, lin(x, w, b)) < 2e-2
+
+
+@pytest.mark.parametrize("cfg", [(128, 128, 64), (64, 64, 32)])
+def test_fp16_tile_configs(gpu, cfg):
+    """fp16 through the Tile API with an explicit tile (the reference's fp16
+    default is 128x128x64, ``kernels/linear.py:208-212``)."""
+    f16 = torch.float16
+    x = randn(4, 150, 136, seed=9, dtype=f16)
+    w = randn(264, 136, seed=10, scale=0.05, dtype=f16)
+    b = randn(264, seed=11, scale=0.1, dtype=f16)
+    op = (tile(x.to(gpu)).with_tile_config(configure_tiles(*cfg))
+          .linear(w.to(gpu), b.to(gpu)))
+    out = op.execute()
+    assert out.dtype == f16
+    assert max_err(out, lin(x, w, b)) < 4e-3
 
 
 def test_layernorm_and_attention_chain(gpu):
