@@ -351,6 +351,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
   constexpr int WNQ = 16 * WCPR / 64;                           // stores per 16-row band
   static_assert(!WSTAGED || (WCPR % 8 == 0 && WNQ * 64 == 16 * WCPR),
                 "wave rows of whole 128-byte lines");
+  static_assert(!WSTAGED || EPI != CGPT_EPI_BIAS_RESID, "no residual epilogue on staged output");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE];
   __shared__ float escr[OUTM == kOutPlain ? NW : 1][OUTM == kOutPlain ? kScrFloats : 1];
   __shared__ __attribute__((aligned(16))) uint8_t sout[WSTAGED ? NW * 16 * WROWB : 16];
@@ -549,6 +550,35 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
           C + static_cast<int64_t>(m0) * ldc, 0,
           static_cast<int>(static_cast<int64_t>(rows) * ldc * static_cast<int64_t>(sizeof(TOut))),
           kBufferRsrcWord3);
+      // Residual epilogue (C += A W^T + bias): every old C value of the tile
+      // is loaded before the first is used (rows past M and columns past N
+      // lie past the resource and read as zero; their stores are dropped).
+      constexpr bool RES = EPI == CGPT_EPI_BIAS_RESID;
+      static_assert(!RES || TM * TN <= 16, "residual epilogue: small tiles only");
+      float cold[RES ? TM : 1][RES ? TN : 1][4];
+      if constexpr (RES) {
+#pragma unroll
+        for (int ii = 0; ii < TM; ++ii) {
+          const uint32_t roff = static_cast<uint32_t>((wm0 + ii * 16 + frow) * ldc);
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            const int n = n0 + wn0 + j * 16 + 4 * fgrp;
+            const uint32_t off =
+                n < N ? (roff + static_cast<uint32_t>(n)) * static_cast<uint32_t>(sizeof(TOut)) : 0x80000000u;
+            if constexpr (sizeof(TOut) == 4) {
+              const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rc, off, 0, 0);
+#pragma unroll
+              for (int r = 0; r < 4; ++r) cold[ii][j][r] = __uint_as_float(v[r]);
+            } else {
+              const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(rc, off, 0, 0);
+              cold[ii][j][0] = __uint_as_float(v[0] << 16);
+              cold[ii][j][1] = __uint_as_float(v[0] & 0xffff0000u);
+              cold[ii][j][2] = __uint_as_float(v[1] << 16);
+              cold[ii][j][3] = __uint_as_float(v[1] & 0xffff0000u);
+            }
+          }
+        }
+      }
 #pragma unroll
       for (int ii = 0; ii < TM; ++ii) {
         const uint32_t roff = static_cast<uint32_t>((wm0 + ii * 16 + frow) * ldc);
@@ -561,6 +591,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
             float t = acc[ii][j][r];
             if (EPI != CGPT_EPI_NONE) t += bias_at(j, r, n);
             if (EPI == CGPT_EPI_BIAS_GELU) t = gelu_tanh(t);
+            if constexpr (RES) t += cold[ii][j][r];
             v[r] = t;
           }
           const uint32_t off =
@@ -584,6 +615,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
           float t = acc[ii][j][r];
           if (EPI != CGPT_EPI_NONE) t += bias_at(j, r, n);
           if (EPI == CGPT_EPI_BIAS_GELU) t = gelu_tanh(t);
+          if (EPI == CGPT_EPI_BIAS_RESID && m < M && n + r < N)
+            t += Elem<TOut>::load(C + static_cast<int64_t>(m) * ldc + n + r);
           v[r] = t;
         }
         if (!vec_store) {
@@ -1279,9 +1312,15 @@ static const TileCfg kBf16Tiles[] = {
     {256, 192, 2, 4},  // 14: 8 waves (128x48), fragment reads one slab ahead, 112 KiB
     {256, 256, 2, 4},  // 15: 8 waves (128x64), SPS 2, 2 stages, rows staged per wave, 160 KiB
     {256, 256, 2, 4},  // 16: 15 with non-temporal output stores
+    {128, 128, 2, 2},  // 17: 4 waves (64x64),  SPS 2, 2 stages, 64 KiB
+    {128, 64, 2, 2},   // 18: 4 waves (64x32),  SPS 2, 3 stages, 72 KiB
+    {64, 64, 2, 2},    // 19: 4 waves (32x32),  SPS 2, 3 stages, 48 KiB
 };
 constexpr int kFirstPipeTile = 5;
-static const int kPipeSps[] = {2, 1, 2, 2, 2, 2, 1, 2, 2, 2, 2, 2};
+static const int kPipeSps[] = {2, 1, 2, 2, 2, 2, 1, 2, 2, 2, 2, 2, 2, 2, 2};
+// Pipelined tiles that also take the residual epilogue (few accumulators a
+// lane, so the tile's old C values fit in registers beside them).
+constexpr int kFirstSmallPipeTile = 17;
 // fp32 configurations (index = tile id for CGPT_F32).
 static const TileCfg kF32Tiles[] = {
     {128, 128, 2, 2},  // 0
@@ -1521,6 +1560,9 @@ static int launch_tile(int tile, const void* a, const void* w, const void* bias,
       case 16:
         return launch_pipe<256, 256, 2, 4, 2, 2, EPI, TOut, kOutWaveStagedNT>(
             a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, s);
+      CGPT_PIPE_CASE(17, 128, 128, 2, 2, 2, 2)
+      CGPT_PIPE_CASE(18, 128, 64, 2, 2, 2, 3)
+      CGPT_PIPE_CASE(19, 64, 64, 2, 2, 2, 3)
       default: return CGPT_EINVAL;
     }
   } else {
@@ -1586,11 +1628,13 @@ static int auto_tile(bool bf16, int M, int N, int K, int64_t lda, int64_t ldw, i
 
 // Residual epilogue (C += A W^T + bias).  `tile`: 14 = the slab kernel's
 // residual ring (bf16 inputs into fp32 C, at least 8 k64 steps, whole
-// 4-column groups, 32-bit offsets; otherwise as TILE_AUTO); a register-staged
-// tile id (bf16 0-4, fp32 0-1) = that tile; anything else = TILE_AUTO: the
-// slab kernel when its 256x192 tiles give at least half the CUs a tile, else
-// the register-staged tile the library's heuristic gives (the largest with
-// 512 blocks, 64x64 below that).
+// 4-column groups, 32-bit offsets; otherwise as TILE_AUTO); 17-19 = that
+// small pipeline tile (bf16, K % 64 == 0; otherwise as TILE_AUTO); a
+// register-staged tile id (bf16 / fp16 0-4, fp32 0-1) = that tile; anything
+// else = TILE_AUTO: the slab kernel when its 256x192 tiles give at least half
+// the CUs a tile, else the 128x64 pipeline (bf16, K % 64 == 0), else the
+// register-staged tile the library's heuristic gives (the largest with 512
+// blocks, 64x64 below that).
 template <typename TIn, typename TOut>
 static int launch_resid(int req_tile, const void* a, const void* w, const void* bias,
                         bool bias_bf16, void* c, int M, int N, int K, int64_t lda, int64_t ldw,
@@ -1598,6 +1642,22 @@ static int launch_resid(int req_tile, const void* a, const void* w, const void* 
   constexpr int EPI = CGPT_EPI_BIAS_RESID;
   const int last = sizeof(TIn) == 2 ? kFirstPipeTile - 1 : kNumF32Tiles - 1;
   const bool reg_tile = req_tile >= 0 && req_tile <= last;
+  if constexpr (std::is_same<TIn, bf16_t>::value) {
+    if (req_tile >= kFirstSmallPipeTile && req_tile < kNumBf16Tiles &&
+        pipe_ok(req_tile, M, N, K, lda, ldw)) {
+      switch (req_tile) {
+        case 17:
+          return launch_pipe<128, 128, 2, 2, 2, 2, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda,
+                                                               ldw, ldc, vec_store, s);
+        case 18:
+          return launch_pipe<128, 64, 2, 2, 2, 3, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda,
+                                                              ldw, ldc, vec_store, s);
+        default:
+          return launch_pipe<64, 64, 2, 2, 2, 3, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda,
+                                                             ldw, ldc, vec_store, s);
+      }
+    }
+  }
   if constexpr (std::is_same<TIn, bf16_t>::value && sizeof(TOut) == 4) {
     const int64_t m = M, n = N;
     const int tiles_m = (M + 255) / 256, tiles_n = (N + 191) / 192;
@@ -1615,6 +1675,14 @@ static int launch_resid(int req_tile, const void* a, const void* w, const void* 
                          tiles_n, vec_store);
       return hip_status(hipGetLastError());
     }
+  }
+  // Too few slab tiles for the CUs: the 128x64 pipeline (4 waves) where K
+  // allows it (medium's 4096x512 projections: 13.0 -> 8.7 and 29.2 -> 20.1
+  // us against the 64x64 register tile).
+  if constexpr (std::is_same<TIn, bf16_t>::value) {
+    if (!reg_tile && pipe_ok(18, M, N, K, lda, ldw))
+      return launch_pipe<128, 64, 2, 2, 2, 3, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda,
+                                                          ldw, ldc, vec_store, s);
   }
   const TileCfg* t = sizeof(TIn) == 2 ? kBf16Tiles : kF32Tiles;
   const int first = sizeof(TIn) == 2 ? (K >= 2048 ? 2 : 3) : 0;

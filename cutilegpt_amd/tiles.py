@@ -28,6 +28,9 @@ Tile ids index the configuration table compiled into libcgpt.so
           15 = 256x256 (8 waves of 128x64)
           16 = the same with non-temporal stores (the LM heads' fp32 logits,
                c_fc + GELU)
+    bf16, the 2-3 stage pipeline with 4 waves on small tiles (also with the
+    residual epilogue; problems whose 256x192 tiles would leave most CUs idle):
+          17 = 128x128 (2 stages)  18 = 128x64 (3 stages)  19 = 64x64 (3 stages)
     fp32: 0 = 128x128, 1 = 64x64
 
 ``TABLE`` maps (dtype, M bucket, N, K) to the tile that won a sweep of every
@@ -39,7 +42,8 @@ a choice.  Anything else falls back to the library's own heuristic
 (``TILE_AUTO``: the persistent tile that fills the 256 CUs best, else the
 register-staged kernel's largest tile giving every CU about two blocks).  For
 the residual epilogue (attn / MLP c_proj into the fp32 residual stream) a
-tile id picks between the slab kernel (14) and the register-staged tiles.
+tile id picks between the slab kernel (14), the small pipeline tiles (17-19)
+and the register-staged tiles.
 """
 
 from __future__ import annotations
@@ -66,9 +70,9 @@ TABLE: Dict[Tuple[int, int, int, int], int] = {
     (_B, 16384, 50304, 768): 16,  # lm head (vocab padded), fp32 out  991
     # 'medium' (8 layers, d 512) prefill, M = 16 x 256
     (_B, 4096, 1536, 512): 14,    # c_attn        463
-    (_B, 4096, 512, 512): 4,      # attn c_proj   161 (64x64: 512 blocks; slab 102)
+    (_B, 4096, 512, 512): 18,     # attn c_proj   248 (128x64 pipeline; 64x64 register 166, slab 104)
     (_B, 4096, 2048, 512): 10,    # c_fc + GELU   520
-    (_B, 4096, 512, 2048): 4,     # mlp c_proj    286 (slab 181)
+    (_B, 4096, 512, 2048): 18,    # mlp c_proj    427 (64x64 register 294, slab 182)
     (_B, 4096, 50304, 512): 16,   # lm head       801
     # GPT-2 XL (48 layers, d 1600) prefill inside generate, M = 32 x 128
     (_B, 4096, 4800, 1600): 14,   # c_attn        961

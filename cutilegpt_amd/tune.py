@@ -13,7 +13,8 @@ Each (shape, tile) is launched ``warmup`` times, then ``iters`` times back to
 back between two HIP events on the launch stream (inputs hot in L2/MALL, the
 same way for every tile).  The residual-epilogue shapes (attn c_proj, MLP
 c_proj: C += A W^T + bias into the fp32 residual stream) sweep the tiles that
-epilogue runs on: the register-staged tiles 0-4 and the slab kernel (14).
+epilogue runs on: the register-staged tiles 0-4, the slab kernel (14) and the
+small pipeline tiles (17-19).
 Needs a GPU.
 """
 
@@ -33,7 +34,7 @@ CONFIGS: Dict[str, Tuple[int, int]] = {
     "xl": (1600, 32 * 128),       # GPT-2 XL prefill inside generate, b32 x 128
 }
 VOCAB_PAD = 50304
-RESID_TILES = [0, 1, 2, 3, 4, 14]
+RESID_TILES = [0, 1, 2, 3, 4, 14, 17, 18, 19]
 
 
 def shapes(name: str) -> List[Tuple[str, int, int, int, int, int]]:

@@ -120,9 +120,9 @@ int cgpt_add_layernorm_partials(const void* x, const float* partials, int64_t n_
  * weight-streaming kernel for M <= 64 rows (decode steps: one row per
  * sequence), CGPT_ESHAPE above; fp32 and bf16 under the vector rules only.
  * With CGPT_EPI_BIAS_RESID (C += A W^T + bias in place, C usually the fp32
- * residual stream), tile 14 asks for the slab kernel's residual ring, a
- * register-staged id (bf16 0-4, fp32 0-1) for that tile, and any other id
- * means CGPT_TILE_AUTO.  A persistent launch (bf16 tile >= 5) over a
+ * residual stream), tile 14 asks for the slab kernel's residual ring, 17-19
+ * for those 4-wave pipeline tiles, a register-staged id (bf16 / fp16 0-4,
+ * fp32 0-1) for that tile, and any other id means CGPT_TILE_AUTO.  A persistent launch (bf16 tile >= 5) over a
  * weight matrix of at least 32 MiB with M >= 1024 first reads W once on the
  * same stream (one extra kernel) so that the launch's repeated W band fetches
  * are served from the memory-side cache.

@@ -176,7 +176,7 @@ def test_gemm_every_bf16_tile(gpu, tile, m, n, k):
     close(out, gemm_ref(a, w, b, _lib.EPI_BIAS), 1e-3, 2 ** -8, f"tile {tile}")
 
 
-DMA_TILES = [5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16]
+DMA_TILES = [5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19]
 
 
 @pytest.mark.parametrize("tile", DMA_TILES)
@@ -193,7 +193,7 @@ def test_gemm_dma_tiles(gpu, tile, m, n, k, epi):
     close(out, ref, 1e-4 * math.sqrt(k / 64), 1e-5, f"dma tile {tile} {m}x{n}x{k}")
 
 
-PERSIST_TILES = [5, 7, 9, 10, 11, 12, 13, 14, 15, 16]
+PERSIST_TILES = [5, 7, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19]
 
 
 @pytest.mark.parametrize("tile", PERSIST_TILES)
@@ -541,9 +541,9 @@ def test_gemm_residual_epilogue_slab(gpu, m, n, k):
 @pytest.mark.parametrize("m,n,k", [(4096, 512, 2048), (300, 520, 512), (513, 200, 640)])
 def test_gemm_residual_epilogue_tiles(gpu, tile, m, n, k):
     """The residual epilogue on every register-staged tile a planner may ask for
-    (and TILE_AUTO, which takes the register kernel when 256x192 slab tiles
-    would leave most CUs idle; a persistent tile id other than 14 means
-    TILE_AUTO): C = C + A W^T + bias against the fp64 sum."""
+    (and TILE_AUTO, which takes the 128x64 pipeline tile when 256x192 slab
+    tiles would leave most CUs idle; a persistent tile id other than 14 and
+    17-19 means TILE_AUTO): C = C + A W^T + bias against the fp64 sum."""
     g = torch.Generator(device=gpu).manual_seed(m + 7 * n + k + tile)
     a = torch.randn(m, k, device=gpu, generator=g).to(BF16)
     w = (torch.randn(n, k, device=gpu, generator=g) * 0.05).to(BF16)
@@ -554,6 +554,26 @@ def test_gemm_residual_epilogue_tiles(gpu, tile, m, n, k):
     _resid_gemm(a, w, b, c, tile=tile)
     err = (c.double() - ref).abs().max().item()
     assert err <= 2e-4 * math.sqrt(k / 64), err
+
+
+@pytest.mark.parametrize("tile", [17, 18, 19])
+@pytest.mark.parametrize("m,n,k,ct", [(4096, 512, 2048, F32), (4096, 1600, 1600, F32),
+                                      (300, 520, 512, F32), (513, 200, 640, F32),
+                                      (1000, 96, 128, BF16), (130, 102, 64, F32)])
+def test_gemm_residual_epilogue_small_pipeline_tiles(gpu, tile, m, n, k, ct):
+    """The residual epilogue on the 4-wave persistent pipeline tiles (the old C
+    values of a tile loaded before its stores; N % 4 != 0 takes per-element
+    stores): against the fp64 sum."""
+    g = torch.Generator(device=gpu).manual_seed(m + 3 * n + k + tile)
+    a = torch.randn(m, k, device=gpu, generator=g).to(BF16)
+    w = (torch.randn(n, k, device=gpu, generator=g) * 0.05).to(BF16)
+    b = torch.randn(n, device=gpu, generator=g).to(BF16)
+    x = (torch.randn(m, n, device=gpu, generator=g) * 4).to(ct)
+    ref = x.double() + a.double() @ w.double().t() + b.double()
+    c = x.clone()
+    _resid_gemm(a, w, b, c, tile=tile)
+    tol = (2e-4 * math.sqrt(k / 64), 1e-6) if ct == F32 else (4e-3, 2 ** -8)
+    close(c, ref, *tol, f"resid tile {tile} {m}x{n}x{k}")
 
 
 @pytest.mark.parametrize("m,n,k,dt,ct", [(77, 130, 96, BF16, F32), (300, 96, 200, BF16, BF16),
