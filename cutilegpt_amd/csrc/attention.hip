@@ -409,19 +409,6 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4,
   const u32x4_t rv = buffer_desc(V + b * v_sb + h * v_sh,
                                  static_cast<uint32_t>((static_cast<int64_t>(Tk - 1) * v_st + HD) * 2));
 
-  u32x4_t qf[QT][NKS];
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    const int qi = q0 + wave * 16 * QT + qt * 16 + frow;
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks)
-      qf[qt][ks] = qi < Tq ? *reinterpret_cast<const u32x4_t*>(Qb + qi * q_st + (4 * ks + g) * 8)
-                           : u32x4_t{0, 0, 0, 0};
-  }
-  // Retire the Q loads here: left to the compiler, the wait would sit before
-  // the first MFMA inside the key loop and drain the DMA queue every block.
-  wait_vmcnt<0>();
-
   const int last_q = min(q0 + BQ, Tq) - 1 + off;
   const int kv_end = causal ? min(last_q + 1, Tk) : Tk;
   const int n_kv = (kv_end + BKV - 1) / BKV;
@@ -479,6 +466,10 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4,
     return __builtin_bit_cast(u32x2_t, r);
   };
 
+  // The first stages' DMA goes out before the Q loads, so the block's first
+  // two memory round trips overlap; one wait then retires both (and keeps the
+  // compiler's own wait for Q, which would sit before the first MFMA inside
+  // the key loop, from draining the DMA queue there).
   int ib = 0;
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
@@ -486,7 +477,16 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4,
       issue(s, smem + s * STAGE);
       ib = s + 1;
     }
-  if (n_kv > 0) wait_later(n_kv - 1 > STAGES - 2 ? STAGES - 2 : n_kv - 1);
+  u32x4_t qf[QT][NKS];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int qi = q0 + wave * 16 * QT + qt * 16 + frow;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks)
+      qf[qt][ks] = qi < Tq ? *reinterpret_cast<const u32x4_t*>(Qb + qi * q_st + (4 * ks + g) * 8)
+                           : u32x4_t{0, 0, 0, 0};
+  }
+  wait_vmcnt<0>();
   int cb = 0;
   for (int j = 0; j < n_kv; ++j) {
     raw_barrier();
