@@ -70,9 +70,9 @@ TABLE: Dict[Tuple[int, int, int, int], int] = {
     (_B, 16384, 50304, 768): 16,  # lm head (vocab padded), fp32 out  991
     # 'medium' (8 layers, d 512) prefill, M = 16 x 256
     (_B, 4096, 1536, 512): 14,    # c_attn        463
-    (_B, 4096, 512, 512): 18,     # attn c_proj   248 (128x64 pipeline; 64x64 register 166, slab 104)
+    (_B, 4096, 512, 512): 18,     # attn c_proj   243 (128x64 pipeline; 64x64 register 162, slab 102)
     (_B, 4096, 2048, 512): 10,    # c_fc + GELU   520
-    (_B, 4096, 512, 2048): 18,    # mlp c_proj    427 (64x64 register 294, slab 182)
+    (_B, 4096, 512, 2048): 18,    # mlp c_proj    427 (64x64 register 292, slab 183)
     (_B, 4096, 50304, 512): 16,   # lm head       801
     # GPT-2 XL (48 layers, d 1600) prefill inside generate, M = 32 x 128
     (_B, 4096, 4800, 1600): 14,   # c_attn        961

@@ -10,8 +10,9 @@ Replaces the reference's fixed per-wrapper tile constants
     python -m cutilegpt_amd.tune [--configs gpt2 medium xl] [--iters 10]
 
 Each (shape, tile) is launched ``warmup`` times, then ``iters`` times back to
-back between two HIP events on the launch stream (inputs hot in L2/MALL, the
-same way for every tile).  The residual-epilogue shapes (attn c_proj, MLP
+back from one captured HIP graph between two HIP events on the launch stream
+(inputs hot in L2/MALL, the same way for every tile; the graph keeps host
+launch overhead out of short kernels' times).  The residual-epilogue shapes (attn c_proj, MLP
 c_proj: C += A W^T + bias into the fp32 residual stream) sweep the tiles that
 epilogue runs on: the register-staged tiles 0-4, the slab kernel (14) and the
 small pipeline tiles (17-19).
@@ -56,7 +57,6 @@ def sweep(name: str, iters: int, warmup: int, out=sys.stdout):
     lib = _lib.load()
     dev = torch.device("cuda:0")
     st = torch.cuda.current_stream(dev)
-    s = st.cuda_stream
     ntiles = lib.cgpt_gemm_num_tiles()
     g = torch.Generator(device=dev).manual_seed(0)
     winners = {}
@@ -72,19 +72,28 @@ def sweep(name: str, iters: int, warmup: int, out=sys.stdout):
         best = None
         for t in tiles:
             def run():
+                # On the current stream: the graph capture below records on its own.
                 return lib.cgpt_gemm(a.data_ptr(), w.data_ptr(), b.data_ptr(), c.data_ptr(), m,
-                                     n, k, k, k, n, _lib.CGPT_BF16, _lib.CGPT_BF16, oc, epi, t, s)
+                                     n, k, k, k, n, _lib.CGPT_BF16, _lib.CGPT_BF16, oc, epi, t,
+                                     torch.cuda.current_stream(dev).cuda_stream)
             if run() != 0:
                 continue
             for _ in range(warmup):
                 run()
+            # The timed launches are replayed from a captured graph, so a short
+            # kernel is not timed at the rate the host can launch it.
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for _ in range(iters):
+                    run()
+            torch.cuda.synchronize()
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
             e0.record(st)
-            for _ in range(iters):
-                run()
+            graph.replay()
             e1.record(st)
             torch.cuda.synchronize()
+            del graph
             ms = e0.elapsed_time(e1) / iters
             rows.append((name, tag, m, n, k, t, ms, fl / ms / 1e9))
             print(f"{name:7s} {tag:12s} M={m:6d} N={n:6d} K={k:5d} tile {t:2d}: "
