@@ -7,7 +7,8 @@ fp16) and the unwired ``TileConfig`` (``cutile_gpt/api/config.py:36-64``).
 Tile ids index the configuration table compiled into libcgpt.so
 (``csrc/gemm.hip``):
 
-    bf16, register-staged double buffer (any K % 8):
+    bf16 (and fp16), register-staged double buffer (any K % 8; other K, strides
+    or alignments take the 64x64 tile with element loads):
           0 = 256x256 (4 waves, 128x128 each), 1 = 256x128, 2 = 128x128,
           3 = 128x64, 4 = 64x64
     bf16, persistent direct-to-LDS pipeline, 8 waves (K % (32 * slabs) == 0):
