@@ -47,7 +47,20 @@ __device__ __forceinline__ void buffer_store4(__amdgpu_buffer_rsrc_t r, uint32_t
   __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])}, r,
                                         off, 0, 0);
 }
+__device__ __forceinline__ void buffer_store4(__amdgpu_buffer_rsrc_t r, uint32_t off, const float* v,
+                                              f16_t*) {
+  __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])}, r,
+                                        off, 0, 0);
+}
 #endif
+
+// The low (hi = false) or high 16-bit element of a 32-bit word as fp32, for a
+// 16-bit type T (bf16 or fp16).
+template <typename T>
+__device__ __forceinline__ float half_word(uint32_t w, bool hi) {
+  if constexpr (std::is_same<T, f16_t>::value) return hi ? f16_hi(w) : f16_lo(w);
+  return __uint_as_float(hi ? (w & 0xffff0000u) : (w << 16));
+}
 
 // `half`: the bias holds 16-bit elements — fp16 when the inputs are fp16,
 // bf16 otherwise — else fp32.
@@ -317,9 +330,10 @@ constexpr int kOutPlain = 0, kOutBuffer = 1, kOutWaveStaged = 2, kOutWaveStagedN
 // with each wave's rows staged through LDS so a store writes whole lines
 // (requires rows of 16-byte multiples), and kOutWaveStagedNT the same with
 // non-temporal stores; kOutPlain — plain stores behind per-lane bounds.
-template <int BM, int BN, int WGM, int WGN, int SPS, int STAGES, int EPI, typename TOut, int OUTM>
+template <int BM, int BN, int WGM, int WGN, int SPS, int STAGES, int EPI, typename TOut, int OUTM,
+          typename TIn = bf16_t>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
-    const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, const void* __restrict__ bias,
+    const TIn* __restrict__ A, const TIn* __restrict__ W, const void* __restrict__ bias,
     bool bias_bf16, TOut* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldw,
     int64_t ldc, int tiles_m, int tiles_n, bool vec_store) {
   // The body uses AMDGPU-only types (buffer resources); the host pass only
@@ -433,7 +447,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) Mfma<bf16_t>::run(f.w[j], f.a[i], acc[i][j]);
+      for (int j = 0; j < TN; ++j) Mfma<TIn>::run(f.w[j], f.a[i], acc[i][j]);
   };
 
   // Bias of a tile, loaded once per tile: tile 0's before the prologue, tile
@@ -475,11 +489,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
     if constexpr (BUFST) {
       if (!bias_bf16) return __uint_as_float(braw[j][r]);
       const uint32_t w = braw[j][r >> 1];
-      return __uint_as_float((r & 1) ? (w & 0xffff0000u) : (w << 16));
+      return half_word<TIn>(w, (r & 1) != 0);
     } else {
       const uint32_t w = braw[j][r];
       if (!bias_bf16) return __uint_as_float(w);
-      return __uint_as_float((min(n + r, N - 1) & 1) ? (w & 0xffff0000u) : (w << 16));
+      return half_word<TIn>(w, (min(n + r, N - 1) & 1) != 0);
     }
   };
   // Returns true when the tile took the buffer-store path, which issues exactly
@@ -527,7 +541,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
             *reinterpret_cast<u32x4_t*>(dst) = u32x4_t{__float_as_uint(v[0]), __float_as_uint(v[1]),
                                                        __float_as_uint(v[2]), __float_as_uint(v[3])};
           } else {
-            *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack2<TOut>(v[0], v[1]), pack2<TOut>(v[2], v[3])};
           }
         }
 #pragma unroll
@@ -571,10 +585,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
               for (int r = 0; r < 4; ++r) cold[ii][j][r] = __uint_as_float(v[r]);
             } else {
               const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(rc, off, 0, 0);
-              cold[ii][j][0] = __uint_as_float(v[0] << 16);
-              cold[ii][j][1] = __uint_as_float(v[0] & 0xffff0000u);
-              cold[ii][j][2] = __uint_as_float(v[1] << 16);
-              cold[ii][j][3] = __uint_as_float(v[1] & 0xffff0000u);
+              cold[ii][j][0] = half_word<TOut>(v[0], false);
+              cold[ii][j][1] = half_word<TOut>(v[0], true);
+              cold[ii][j][2] = half_word<TOut>(v[1], false);
+              cold[ii][j][3] = half_word<TOut>(v[1], true);
             }
           }
         }
@@ -702,9 +716,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(
 // each step issues W(g+1) then A(g+2), so the A rows — most of an XCD's L2
 // misses, since each A block is shared by 4 CUs of a round and each W block
 // by 8 — get two steps to arrive.  k = 64 per stage (SPS 2).
-template <int BM, int BN, int WGM, int WGN, int EPI, typename TOut>
+template <int BM, int BN, int WGM, int WGN, int EPI, typename TOut, typename TIn = bf16_t>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_a3_kernel(
-    const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, const void* __restrict__ bias,
+    const TIn* __restrict__ A, const TIn* __restrict__ W, const void* __restrict__ bias,
     bool bias_bf16, TOut* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldw,
     int64_t ldc, int tiles_m, int tiles_n, bool vec_store) {
   // The body uses AMDGPU-only types (buffer resources); the host pass only
@@ -816,7 +830,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_a3_kernel(
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) Mfma<bf16_t>::run(f.w[j], f.a[i], acc[i][j]);
+      for (int j = 0; j < TN; ++j) Mfma<TIn>::run(f.w[j], f.a[i], acc[i][j]);
   };
 
   // Bias of a tile, loaded once per tile as in gemm_pipe_kernel (N % 4 == 0:
@@ -839,7 +853,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_a3_kernel(
   auto bias_at = [&](int j, int r) -> float {
     if (!bias_bf16) return __uint_as_float(braw[j][r]);
     const uint32_t w = braw[j][r >> 1];
-    return __uint_as_float((r & 1) ? (w & 0xffff0000u) : (w << 16));
+    return half_word<TIn>(w, (r & 1) != 0);
   };
   // Exactly TM * TN buffer stores per wave: rows past M lie past the
   // resource's size and columns past N get an offset past it, so both are
@@ -947,9 +961,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_a3_kernel(
 constexpr int kSlabStorePolicy = 2;
 constexpr int kResidMinSteps = 8;  // k64 steps a tile needs for the residual ring
 
-template <int BM, int BN, int WGM, int WGN, int EPI, typename TOut>
+template <int BM, int BN, int WGM, int WGN, int EPI, typename TOut, typename TIn = bf16_t>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_slab_kernel(
-    const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, const void* __restrict__ bias,
+    const TIn* __restrict__ A, const TIn* __restrict__ W, const void* __restrict__ bias,
     bool bias_bf16, TOut* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldw,
     int64_t ldc, int tiles_m, int tiles_n, bool vec_store) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -1118,7 +1132,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_slab_kernel(
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) Mfma<bf16_t>::run(f.w[j], f.a[i], acc[i][j]);
+      for (int j = 0; j < TN; ++j) Mfma<TIn>::run(f.w[j], f.a[i], acc[i][j]);
   };
 
   uint32_t braw[TN][4];
@@ -1139,7 +1153,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_slab_kernel(
   auto bias_at = [&](int j, int r) -> float {
     if (!bias_bf16) return __uint_as_float(braw[j][r]);
     const uint32_t w = braw[j][r >> 1];
-    return __uint_as_float((r & 1) ? (w & 0xffff0000u) : (w << 16));
+    return half_word<TIn>(w, (r & 1) != 0);
   };
   // Epilogue through LDS: each pass writes IIP row bands of every wave (bias
   // and GELU applied) into sout, barrier, then every thread stores CH_PER_T
@@ -1208,7 +1222,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_slab_kernel(
             *reinterpret_cast<u32x4_t*>(dst) = u32x4_t{__float_as_uint(v[0]), __float_as_uint(v[1]),
                                                        __float_as_uint(v[2]), __float_as_uint(v[3])};
           } else {
-            *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack2<TOut>(v[0], v[1]), pack2<TOut>(v[2], v[3])};
           }
         }
       }
@@ -1362,7 +1376,7 @@ static int num_cus() {
 // WSO: 0 = buffer (or plain) stores, else the wave-staged output mode to use
 // where the output allows it (kOutWaveStaged or kOutWaveStagedNT).
 template <int BM, int BN, int WGM, int WGN, int SPS, int STAGES, int EPI, typename TOut,
-          int WSO = 0>
+          int WSO = 0, typename TIn = bf16_t>
 static int launch_pipe(const void* a, const void* w, const void* bias, bool bias_bf16, void* c,
                        int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc, bool vec_store,
                        hipStream_t s) {
@@ -1386,22 +1400,22 @@ static int launch_pipe(const void* a, const void* w, const void* bias, bool bias
                       reinterpret_cast<uintptr_t>(c) % 16 == 0;
   if constexpr (WSO != 0) {
     if (staged) {
-      hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut, WSO>),
-                         dim3(grid), dim3(64 * WGM * WGN), 0, s, static_cast<const bf16_t*>(a),
-                         static_cast<const bf16_t*>(w), bias, bias_bf16, static_cast<TOut*>(c), M,
+      hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut, WSO, TIn>),
+                         dim3(grid), dim3(64 * WGM * WGN), 0, s, static_cast<const TIn*>(a),
+                         static_cast<const TIn*>(w), bias, bias_bf16, static_cast<TOut*>(c), M,
                          N, K, lda, ldw, ldc, tiles_m, tiles_n, vec_store);
       return hip_status(hipGetLastError());
     }
   }
   if (buf_store)
-    hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut, kOutBuffer>), dim3(grid),
-                       dim3(64 * WGM * WGN), 0, s, static_cast<const bf16_t*>(a),
-                       static_cast<const bf16_t*>(w), bias, bias_bf16, static_cast<TOut*>(c), M, N,
+    hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut, kOutBuffer, TIn>), dim3(grid),
+                       dim3(64 * WGM * WGN), 0, s, static_cast<const TIn*>(a),
+                       static_cast<const TIn*>(w), bias, bias_bf16, static_cast<TOut*>(c), M, N,
                        K, lda, ldw, ldc, tiles_m, tiles_n, vec_store);
   else
-    hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut, kOutPlain>), dim3(grid),
-                       dim3(64 * WGM * WGN), 0, s, static_cast<const bf16_t*>(a),
-                       static_cast<const bf16_t*>(w), bias, bias_bf16, static_cast<TOut*>(c), M, N,
+    hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut, kOutPlain, TIn>), dim3(grid),
+                       dim3(64 * WGM * WGN), 0, s, static_cast<const TIn*>(a),
+                       static_cast<const TIn*>(w), bias, bias_bf16, static_cast<TOut*>(c), M, N,
                        K, lda, ldw, ldc, tiles_m, tiles_n, vec_store);
   return hip_status(hipGetLastError());
 }
@@ -1409,7 +1423,7 @@ static int launch_pipe(const void* a, const void* w, const void* bias, bool bias
 // A fetched two steps ahead (3 A buffers, 2 W buffers, k = 64 per stage).  It
 // only has the buffer-store epilogue; other output layouts take the two-stage
 // kernel of the same tile.
-template <int BM, int BN, int WGM, int WGN, int EPI, typename TOut>
+template <int BM, int BN, int WGM, int WGN, int EPI, typename TOut, typename TIn = bf16_t>
 static int launch_pipe_a3(const void* a, const void* w, const void* bias, bool bias_bf16, void* c,
                           int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc,
                           bool vec_store, hipStream_t s) {
@@ -1417,16 +1431,16 @@ static int launch_pipe_a3(const void* a, const void* w, const void* bias, bool b
   const bool buf_store = vec_store && N % 4 == 0 &&
                          static_cast<int64_t>(BM) * ldc * static_cast<int64_t>(sizeof(TOut)) < 0x7fffffff;
   if (!buf_store)
-    return launch_pipe<BM, BN, WGM, WGN, 2, 2, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda,
-                                                          ldw, ldc, vec_store, s);
+    return launch_pipe<BM, BN, WGM, WGN, 2, 2, EPI, TOut, 0, TIn>(a, w, bias, bias_bf16, c, M, N, K,
+                                                                  lda, ldw, ldc, vec_store, s);
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = (N + BN - 1) / BN;
   const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
   if (tiles > 0x7fffffff) return CGPT_ESHAPE;
   const int grid = static_cast<int>(tiles < num_cus() ? tiles : num_cus());
-  hipLaunchKernelGGL((gemm_pipe_a3_kernel<BM, BN, WGM, WGN, EPI, TOut>), dim3(grid),
-                     dim3(64 * WGM * WGN), 0, s, static_cast<const bf16_t*>(a),
-                     static_cast<const bf16_t*>(w), bias, bias_bf16, static_cast<TOut*>(c), M, N,
+  hipLaunchKernelGGL((gemm_pipe_a3_kernel<BM, BN, WGM, WGN, EPI, TOut, TIn>), dim3(grid),
+                     dim3(64 * WGM * WGN), 0, s, static_cast<const TIn*>(a),
+                     static_cast<const TIn*>(w), bias, bias_bf16, static_cast<TOut*>(c), M, N,
                      K, lda, ldw, ldc, tiles_m, tiles_n, vec_store);
   return hip_status(hipGetLastError());
 }
@@ -1435,7 +1449,7 @@ static int launch_pipe_a3(const void* a, const void* w, const void* bias, bool b
 // take the two-stage pipeline kernel of the same tile).  Its source offsets
 // are not clamped to the last row, so a whole tile past M (or N) must still
 // address below 4 GiB.
-template <int BM, int BN, int WGM, int WGN, int EPI, typename TOut>
+template <int BM, int BN, int WGM, int WGN, int EPI, typename TOut, typename TIn = bf16_t>
 static int launch_slab(const void* a, const void* w, const void* bias, bool bias_bf16, void* c,
                        int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc, bool vec_store,
                        hipStream_t s) {
@@ -1443,8 +1457,8 @@ static int launch_slab(const void* a, const void* w, const void* bias, bool bias
       (static_cast<int64_t>(N) + BN) * ldw * 2 >= (int64_t{1} << 32) ||
       static_cast<int64_t>(BM) * lda * 2 >= (int64_t{1} << 31) ||
       static_cast<int64_t>(BN) * ldw * 2 >= (int64_t{1} << 31))
-    return launch_pipe<BM, BN, WGM, WGN, 2, 2, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda,
-                                                          ldw, ldc, vec_store, s);
+    return launch_pipe<BM, BN, WGM, WGN, 2, 2, EPI, TOut, 0, TIn>(a, w, bias, bias_bf16, c, M, N, K,
+                                                                  lda, ldw, ldc, vec_store, s);
   static_assert(2 * (BM + BN) * 128 < 160 * 1024, "LDS budget of one CU");
   // Whole 16-byte chunks: N and ldc multiples of 16 bytes' worth of elements
   // and a 16-byte aligned C (vec_store guarantees only 8 bytes for bf16).
@@ -1453,16 +1467,16 @@ static int launch_slab(const void* a, const void* w, const void* bias, bool bias
                          reinterpret_cast<uintptr_t>(c) % 16 == 0 &&
                          static_cast<int64_t>(BM) * ldc * static_cast<int64_t>(sizeof(TOut)) < 0x7fffffff;
   if (!buf_store)
-    return launch_pipe<BM, BN, WGM, WGN, 2, 2, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda,
-                                                          ldw, ldc, vec_store, s);
+    return launch_pipe<BM, BN, WGM, WGN, 2, 2, EPI, TOut, 0, TIn>(a, w, bias, bias_bf16, c, M, N, K,
+                                                                  lda, ldw, ldc, vec_store, s);
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = (N + BN - 1) / BN;
   const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
   if (tiles > 0x7fffffff) return CGPT_ESHAPE;
   const int grid = static_cast<int>(tiles < num_cus() ? tiles : num_cus());
-  hipLaunchKernelGGL((gemm_slab_kernel<BM, BN, WGM, WGN, EPI, TOut>), dim3(grid),
-                     dim3(64 * WGM * WGN), 0, s, static_cast<const bf16_t*>(a),
-                     static_cast<const bf16_t*>(w), bias, bias_bf16, static_cast<TOut*>(c), M, N,
+  hipLaunchKernelGGL((gemm_slab_kernel<BM, BN, WGM, WGN, EPI, TOut, TIn>), dim3(grid),
+                     dim3(64 * WGM * WGN), 0, s, static_cast<const TIn*>(a),
+                     static_cast<const TIn*>(w), bias, bias_bf16, static_cast<TOut*>(c), M, N,
                      K, lda, ldw, ldc, tiles_m, tiles_n, vec_store);
   return hip_status(hipGetLastError());
 }
@@ -1517,21 +1531,12 @@ static int launch_tile(int tile, const void* a, const void* w, const void* bias,
   case id:                                                                                    \
     return launch_cfg<TIn, BM, BN, WGM, WGN, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda, \
                                                         ldw, ldc, vec_store, s);
-#define CGPT_PIPE_CASE(id, BM, BN, WGM, WGN, SPS, ST)                                          \
-  case id:                                                                                     \
-    return launch_pipe<BM, BN, WGM, WGN, SPS, ST, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, \
-                                                             lda, ldw, ldc, vec_store, s);
-  if constexpr (std::is_same<TIn, f16_t>::value) {
-    // fp16: the register-staged tiles (the pipelines are bf16 only).
-    switch (tile) {
-      CGPT_GEMM_CASE(0, 256, 256, 2, 2)
-      CGPT_GEMM_CASE(1, 256, 128, 2, 2)
-      CGPT_GEMM_CASE(2, 128, 128, 2, 2)
-      CGPT_GEMM_CASE(3, 128, 64, 2, 2)
-      CGPT_GEMM_CASE(4, 64, 64, 2, 2)
-      default: return CGPT_EINVAL;
-    }
-  } else if constexpr (sizeof(TIn) == 2) {
+#define CGPT_PIPE_CASE(id, BM, BN, WGM, WGN, SPS, ST)                                           \
+  case id:                                                                                      \
+    return launch_pipe<BM, BN, WGM, WGN, SPS, ST, EPI, TOut, 0, TIn>(a, w, bias, bias_bf16, c, M, \
+                                                                     N, K, lda, ldw, ldc,         \
+                                                                     vec_store, s);
+  if constexpr (sizeof(TIn) == 2) {
     switch (tile) {
       CGPT_GEMM_CASE(0, 256, 256, 2, 2)
       CGPT_GEMM_CASE(1, 256, 128, 2, 2)
@@ -1546,19 +1551,19 @@ static int launch_tile(int tile, const void* a, const void* w, const void* bias,
       CGPT_PIPE_CASE(10, 128, 256, 2, 4, 2, 3)
       CGPT_PIPE_CASE(11, 256, 128, 4, 2, 1, 6)
       case 12:
-        return launch_pipe_a3<256, 256, 2, 4, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda,
+        return launch_pipe_a3<256, 256, 2, 4, EPI, TOut, TIn>(a, w, bias, bias_bf16, c, M, N, K, lda,
                                                          ldw, ldc, vec_store, s);
       case 13:
-        return launch_pipe_a3<256, 192, 2, 4, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda,
+        return launch_pipe_a3<256, 192, 2, 4, EPI, TOut, TIn>(a, w, bias, bias_bf16, c, M, N, K, lda,
                                                          ldw, ldc, vec_store, s);
       case 14:
-        return launch_slab<256, 192, 2, 4, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda, ldw,
+        return launch_slab<256, 192, 2, 4, EPI, TOut, TIn>(a, w, bias, bias_bf16, c, M, N, K, lda, ldw,
                                                       ldc, vec_store, s);
       case 15:
-        return launch_pipe<256, 256, 2, 4, 2, 2, EPI, TOut, kOutWaveStaged>(
+        return launch_pipe<256, 256, 2, 4, 2, 2, EPI, TOut, kOutWaveStaged, TIn>(
             a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, s);
       case 16:
-        return launch_pipe<256, 256, 2, 4, 2, 2, EPI, TOut, kOutWaveStagedNT>(
+        return launch_pipe<256, 256, 2, 4, 2, 2, EPI, TOut, kOutWaveStagedNT, TIn>(
             a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, s);
       CGPT_PIPE_CASE(17, 128, 128, 2, 2, 2, 2)
       CGPT_PIPE_CASE(18, 128, 64, 2, 2, 2, 3)
@@ -1579,9 +1584,8 @@ static int launch_tile(int tile, const void* a, const void* w, const void* bias,
 // Default tile choice when the caller's table has no entry: the register-staged
 // kernel with the largest tile that still gives every CU about two blocks
 // (128x128 for long K, 128x64 otherwise), smaller tiles for small grids.
-static int auto_tile(bool bf16, int M, int N, int K, int64_t lda, int64_t ldw, int epi,
-                     bool pipes = true) {
-  // bf16 problems with at least one 256x192 tile per CU: the persistent
+static int auto_tile(bool half, int M, int N, int K, int64_t lda, int64_t ldw, int epi) {
+  // 16-bit (bf16 / fp16) problems with at least one 256x192 tile per CU: the persistent
   // direct-to-LDS pipelines — 256x256 with wave-staged non-temporal stores
   // for wide N (the LM heads) and for the GELU epilogue; 256x192 with
   // block-staged stores otherwise.  With fewer
@@ -1589,7 +1593,7 @@ static int auto_tile(bool bf16, int M, int N, int K, int64_t lda, int64_t ldw, i
   // last round leaves the fewest CUs idle (ties to the larger tile), as long
   // as it still gives half the CUs a tile; below that the register-staged
   // kernel with smaller tiles.
-  if (bf16 && pipes) {
+  if (half) {
     auto tiles = [&](int bm, int bn) {
       return static_cast<int64_t>((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     };
@@ -1614,10 +1618,10 @@ static int auto_tile(bool bf16, int M, int N, int K, int64_t lda, int64_t ldw, i
       if (best >= 0) return best;
     }
   }
-  const TileCfg* t = bf16 ? kBf16Tiles : kF32Tiles;
-  const int nt = bf16 ? kNumBf16Tiles : kNumF32Tiles;
-  const int first = bf16 ? (K >= 2048 ? 2 : 3) : 0;
-  const int last = bf16 ? kFirstPipeTile - 1 : nt - 1;
+  const TileCfg* t = half ? kBf16Tiles : kF32Tiles;
+  const int nt = half ? kNumBf16Tiles : kNumF32Tiles;
+  const int first = half ? (K >= 2048 ? 2 : 3) : 0;
+  const int last = half ? kFirstPipeTile - 1 : nt - 1;
   for (int i = first; i <= last; ++i) {
     const int64_t blocks =
         static_cast<int64_t>((M + t[i].bm - 1) / t[i].bm) * ((N + t[i].bn - 1) / t[i].bn);
@@ -1642,23 +1646,23 @@ static int launch_resid(int req_tile, const void* a, const void* w, const void* 
   constexpr int EPI = CGPT_EPI_BIAS_RESID;
   const int last = sizeof(TIn) == 2 ? kFirstPipeTile - 1 : kNumF32Tiles - 1;
   const bool reg_tile = req_tile >= 0 && req_tile <= last;
-  if constexpr (std::is_same<TIn, bf16_t>::value) {
+  if constexpr (sizeof(TIn) == 2) {
     if (req_tile >= kFirstSmallPipeTile && req_tile < kNumBf16Tiles &&
         pipe_ok(req_tile, M, N, K, lda, ldw)) {
       switch (req_tile) {
         case 17:
-          return launch_pipe<128, 128, 2, 2, 2, 2, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda,
-                                                               ldw, ldc, vec_store, s);
+          return launch_pipe<128, 128, 2, 2, 2, 2, EPI, TOut, 0, TIn>(a, w, bias, bias_bf16, c, M, N,
+                                                                      K, lda, ldw, ldc, vec_store, s);
         case 18:
-          return launch_pipe<128, 64, 2, 2, 2, 3, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda,
-                                                              ldw, ldc, vec_store, s);
+          return launch_pipe<128, 64, 2, 2, 2, 3, EPI, TOut, 0, TIn>(a, w, bias, bias_bf16, c, M, N,
+                                                                     K, lda, ldw, ldc, vec_store, s);
         default:
-          return launch_pipe<64, 64, 2, 2, 2, 3, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda,
-                                                             ldw, ldc, vec_store, s);
+          return launch_pipe<64, 64, 2, 2, 2, 3, EPI, TOut, 0, TIn>(a, w, bias, bias_bf16, c, M, N,
+                                                                    K, lda, ldw, ldc, vec_store, s);
       }
     }
   }
-  if constexpr (std::is_same<TIn, bf16_t>::value && sizeof(TOut) == 4) {
+  if constexpr (sizeof(TIn) == 2 && sizeof(TOut) == 4) {
     const int64_t m = M, n = N;
     const int tiles_m = (M + 255) / 256, tiles_n = (N + 191) / 192;
     const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
@@ -1669,8 +1673,8 @@ static int launch_resid(int req_tile, const void* a, const void* w, const void* 
         256 * ldc * 4 < 0x7fffffff) {
       if (tiles > 0x7fffffff) return CGPT_ESHAPE;
       const int grid = static_cast<int>(tiles < num_cus() ? tiles : num_cus());
-      hipLaunchKernelGGL((gemm_slab_kernel<256, 192, 2, 4, EPI, float>), dim3(grid), dim3(512), 0,
-                         s, static_cast<const bf16_t*>(a), static_cast<const bf16_t*>(w), bias,
+      hipLaunchKernelGGL((gemm_slab_kernel<256, 192, 2, 4, EPI, float, TIn>), dim3(grid), dim3(512),
+                         0, s, static_cast<const TIn*>(a), static_cast<const TIn*>(w), bias,
                          bias_bf16, static_cast<float*>(c), M, N, K, lda, ldw, ldc, tiles_m,
                          tiles_n, vec_store);
       return hip_status(hipGetLastError());
@@ -1679,10 +1683,10 @@ static int launch_resid(int req_tile, const void* a, const void* w, const void* 
   // Too few slab tiles for the CUs: the 128x64 pipeline (4 waves) where K
   // allows it (medium's 4096x512 projections: 13.0 -> 8.7 and 29.2 -> 20.1
   // us against the 64x64 register tile).
-  if constexpr (std::is_same<TIn, bf16_t>::value) {
+  if constexpr (sizeof(TIn) == 2) {
     if (!reg_tile && pipe_ok(18, M, N, K, lda, ldw))
-      return launch_pipe<128, 64, 2, 2, 2, 3, EPI, TOut>(a, w, bias, bias_bf16, c, M, N, K, lda,
-                                                          ldw, ldc, vec_store, s);
+      return launch_pipe<128, 64, 2, 2, 2, 3, EPI, TOut, 0, TIn>(a, w, bias, bias_bf16, c, M, N, K,
+                                                                 lda, ldw, ldc, vec_store, s);
   }
   const TileCfg* t = sizeof(TIn) == 2 ? kBf16Tiles : kF32Tiles;
   const int first = sizeof(TIn) == 2 ? (K >= 2048 ? 2 : 3) : 0;
@@ -1865,7 +1869,7 @@ extern "C" int cgpt_gemm(const void* a, const void* w, const void* bias, void* c
                                out_dtype, epilogue, &el);
   if (st != CGPT_OK || M == 0 || N == 0) return st;
   const bool bf16 = in_dtype == CGPT_BF16, f16 = in_dtype == CGPT_F16;
-  const int nt = bf16 ? kNumBf16Tiles : f16 ? kFirstPipeTile : kNumF32Tiles;
+  const int nt = (bf16 || f16) ? kNumBf16Tiles : kNumF32Tiles;
   const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bb = bias_dtype != CGPT_F32;
@@ -1906,9 +1910,10 @@ extern "C" int cgpt_gemm(const void* a, const void* w, const void* bias, void* c
                               nullptr, 0, nullptr, 0, s);
   }
   if (el) tile = 0;  // the element-load kernel has one tile
-  if (tile == CGPT_TILE_AUTO) tile = auto_tile(bf16 || f16, m, n, k, lda, ldw, epilogue, !f16);
-  if (bf16 && tile >= kFirstPipeTile && !pipe_ok(tile, M, N, K, lda, ldw)) return CGPT_ESHAPE;
-  if (bf16 && tile >= kFirstPipeTile) {
+  if (tile == CGPT_TILE_AUTO) tile = auto_tile(bf16 || f16, m, n, k, lda, ldw, epilogue);
+  if ((bf16 || f16) && tile >= kFirstPipeTile && !pipe_ok(tile, M, N, K, lda, ldw))
+    return CGPT_ESHAPE;
+  if ((bf16 || f16) && tile >= kFirstPipeTile) {
     const int pst = maybe_prefetch_w(w, M, N, K, ldw, s);
     if (pst != CGPT_OK) return pst;
   }

@@ -7,8 +7,9 @@ fp16) and the unwired ``TileConfig`` (``cutile_gpt/api/config.py:36-64``).
 Tile ids index the configuration table compiled into libcgpt.so
 (``csrc/gemm.hip``):
 
-    bf16 (and fp16), register-staged double buffer (any K % 8; other K, strides
-    or alignments take the 64x64 tile with element loads):
+    bf16 (every id below also runs fp16 inputs on the fp16 MFMA), register-staged
+    double buffer (any K % 8; other K, strides or alignments take the 64x64 tile
+    with element loads):
           0 = 256x256 (4 waves, 128x128 each), 1 = 256x128, 2 = 128x128,
           3 = 128x64, 4 = 64x64
     bf16, persistent direct-to-LDS pipeline, 8 waves (K % (32 * slabs) == 0):
@@ -86,5 +87,8 @@ TABLE: Dict[Tuple[int, int, int, int], int] = {
 
 def gemm_tile(dtype_code: int, m: int, n: int, k: int) -> int:
     """Tile id for a GEMM problem (table hit for M's bucket, else the library
-    heuristic)."""
+    heuristic).  fp16 inputs run the bf16 kernels on the fp16 MFMA at the same
+    rate, so they share the bf16 entries."""
+    if dtype_code == _lib.CGPT_F16:
+        dtype_code = _lib.CGPT_BF16
     return TABLE.get((dtype_code, m_bucket(m), n, k), _lib.TILE_AUTO)

@@ -113,8 +113,8 @@ int cgpt_add_layernorm_partials(const void* x, const float* partials, int64_t n_
  * pointers: problems with K, lda and ldw multiples of 8 (16-bit) or 4 (fp32)
  * elements and 16-byte aligned A, W and bias take the vector kernels below;
  * others run a 64x64 register-staged kernel that loads element by element
- * (any tile id but CGPT_TILE_SKINNY is then ignored).  fp16 runs the
- * register-staged tiles 0-4 only.
+ * (any tile id but CGPT_TILE_SKINNY is then ignored).  fp16 inputs run every
+ * tile id as bf16 does, on the fp16 MFMA.
  * `tile` selects a tile configuration: CGPT_TILE_AUTO = library heuristic (the
  * skinny kernel when M <= 64, fp32 / bf16); CGPT_TILE_SKINNY = the
  * weight-streaming kernel for M <= 64 rows (decode steps: one row per

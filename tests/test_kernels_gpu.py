@@ -201,15 +201,18 @@ PERSIST_TILES = [5, 7, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19]
                                    (16384, 768, 3072), (1, 3, 128), (1000, 1000, 64),
                                    (2000, 50304, 64)])
 @pytest.mark.parametrize("epi", [_lib.EPI_BIAS, _lib.EPI_BIAS_GELU])
-def test_gemm_persistent_tiles(gpu, tile, m, n, k, epi):
+@pytest.mark.parametrize("dtype", [BF16, torch.float16])
+def test_gemm_persistent_tiles(gpu, tile, m, n, k, epi, dtype):
     """Persistent kernel: several tiles per block (tile boundaries inside the
-    flattened K stream), fewer tiles than CUs, ragged edges."""
-    a = randn(m, k, seed=21, dtype=BF16)
-    w = randn(n, k, seed=22, dtype=BF16, scale=0.05)
-    b = randn(n, seed=23, dtype=BF16)
-    out = cg.kernels._gemm(a.to(gpu), w.to(gpu), b.to(gpu), epi, BF16, "t", tile=tile)
+    flattened K stream), fewer tiles than CUs, ragged edges; bf16 and fp16
+    inputs (the fp16 MFMA and fp16 bias / outputs)."""
+    a = randn(m, k, seed=21, dtype=dtype)
+    w = randn(n, k, seed=22, dtype=dtype, scale=0.05)
+    b = randn(n, seed=23, dtype=dtype)
+    out = cg.kernels._gemm(a.to(gpu), w.to(gpu), b.to(gpu), epi, dtype, "t", tile=tile)
     ref = gemm_ref(a, w, b, epi)
-    close(out, ref, 2e-3, 2 ** -8, f"persistent tile {tile} {m}x{n}x{k}")
+    close(out, ref, 2e-3, 2 ** -8 if dtype == BF16 else 2 ** -10,
+          f"persistent tile {tile} {m}x{n}x{k} {dtype}")
 
 
 @pytest.mark.parametrize("tile", [14, 15, 16])

@@ -93,9 +93,11 @@ def test_gemm_fp16(gpu, m, n, k, epi, out_dtype):
           f"fp16 gemm {m}x{n}x{k} epi{epi}")
 
 
-@pytest.mark.parametrize("tile", range(5))
+@pytest.mark.parametrize("tile", range(20))
 def test_gemm_fp16_every_tile_and_fp32_bias(gpu, tile):
-    m, n, k = 300, 264, 520
+    """Every tile id on fp16 inputs: the register-staged tiles (0-4) and the
+    persistent pipelines (5-19, K a multiple of 64), fp32 bias, fp16 out."""
+    m, n, k = 300, 264, 520 if tile < 5 else 512
     a = randn(m, k, seed=1, dtype=F16)
     w = randn(n, k, seed=2, dtype=F16, scale=0.05)
     b = randn(n, seed=3, dtype=F32)
@@ -105,22 +107,26 @@ def test_gemm_fp16_every_tile_and_fp32_bias(gpu, tile):
     close(c, gemm_ref(a, w, b, _lib.EPI_BIAS), 2e-3, 2 ** -11, f"fp16 tile {tile}")
 
 
-def test_gemm_fp16_residual_epilogue(gpu):
-    m, n, k = 1000, 768, 768
+@pytest.mark.parametrize("tile,m", [(_lib.TILE_AUTO, 1000), (14, 2048), (17, 1000), (4, 1000)])
+def test_gemm_fp16_residual_epilogue(gpu, tile, m):
+    """C += A W^T + bias into fp32 C from fp16 inputs: the slab kernel's residual
+    ring (14), the 4-wave pipeline (TILE_AUTO at this size takes 18; 17) and a
+    register-staged tile."""
+    n, k = 768, 768
     a = randn(m, k, seed=4, dtype=F16)
     w = randn(n, k, seed=5, dtype=F16, scale=0.05)
     b = randn(n, seed=6, dtype=F16)
     c0 = randn(m, n, seed=7, dtype=F32)
     c = c0.to(gpu)
     gemm_raw(a.to(gpu), w.to(gpu), b.to(gpu), c, _lib.EPI_BIAS_RESID, _lib.CGPT_F16,
-             _lib.CGPT_F16, _lib.CGPT_F32)
+             _lib.CGPT_F16, _lib.CGPT_F32, tile)
     close(c, gemm_ref(a, w, b, _lib.EPI_BIAS_RESID, c0), 2e-4 * math.sqrt(k / 64), 1e-6,
-          "fp16 resid")
+          f"fp16 resid tile {tile}")
 
 
 def test_gemm_fp16_dtype_rules(gpu):
-    """fp16 inputs take fp16 / fp32 bias and outputs, not bf16; no pipeline or
-    skinny tile."""
+    """fp16 inputs take fp16 / fp32 bias and outputs, not bf16; no skinny tile
+    and no tile id past the table."""
     lib = _lib.load()
     a = torch.zeros(64, 64, dtype=F16, device=gpu)
     c = torch.zeros(64, 64, dtype=F16, device=gpu)
@@ -130,7 +136,7 @@ def test_gemm_fp16_dtype_rules(gpu):
                                               out_code, _lib.EPI_BIAS, tile, s)
     assert lib.cgpt_gemm(*args(_lib.CGPT_BF16, _lib.CGPT_F16, -1)) == -2
     assert lib.cgpt_gemm(*args(_lib.CGPT_F16, _lib.CGPT_BF16, -1)) == -2
-    assert lib.cgpt_gemm(*args(_lib.CGPT_F16, _lib.CGPT_F16, 14)) == -1
+    assert lib.cgpt_gemm(*args(_lib.CGPT_F16, _lib.CGPT_F16, lib.cgpt_gemm_num_tiles())) == -1
     assert lib.cgpt_gemm(*args(_lib.CGPT_F16, _lib.CGPT_F16, _lib.TILE_SKINNY)) == -1
     torch.cuda.synchronize()
 
