@@ -367,16 +367,17 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
 //    of the P operand (keys 32c + 4g + r, then 32c + 16 + 4g + r).
 //  * 16-byte chunk c of row r is stored at chunk c ^ (r & 7): the DMA lane
 //    that fills a slot fetches the chunk that belongs there.
-template <int HD, int STAGES, int QTW>
+template <int HD, int STAGES, int QTW, typename T = bf16_t>
 // Four waves per SIMD (VGPRs capped at 128; two 32 KiB stages per block, so
 // four 128-query blocks fit a CU's LDS): 576 -> 620 TFLOP/s at 16x12x1024x64
 // against three waves and three stages, bit-identical.
 __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void attn_fwd_dma_kernel(
-    const bf16_t* __restrict__ Q, const bf16_t* __restrict__ K, const bf16_t* __restrict__ V,
-    bf16_t* __restrict__ O, int H, int Tq, int Tk, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
+    T* __restrict__ O, int H, int Tq, int Tk, int64_t q_sb, int64_t q_sh, int64_t q_st,
     int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st,
     int64_t o_sb, int64_t o_sh, int64_t o_st, float scale_log2, int causal, int n_bh) {
 #if defined(__HIP_DEVICE_COMPILE__)
+  static_assert(sizeof(T) == 2, "16-bit inputs (bf16 or fp16)");
   constexpr int QT = QTW, BQ = 4 * 16 * QTW, BKV = kAttnBKV;
   constexpr int NWAVE = kAttnThreads / 64;
   constexpr int KROW = HD * 2;                 // bytes per K / V row
@@ -403,7 +404,7 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4,
   const int q0 = qb * BQ;
   const int off = Tk - Tq;
 
-  const bf16_t* Qb = Q + b * q_sb + h * q_sh;
+  const T* Qb = Q + b * q_sb + h * q_sh;
   const u32x4_t rk = buffer_desc(K + b * k_sb + h * k_sh,
                                  static_cast<uint32_t>((static_cast<int64_t>(Tk - 1) * k_st + HD) * 2));
   const u32x4_t rv = buffer_desc(V + b * v_sb + h * v_sh,
@@ -513,7 +514,7 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4,
           const u32x4_t kf =
               *reinterpret_cast<const u32x4_t*>(sk + key * KROW + ((c ^ (key & 7)) << 4));
 #pragma unroll
-          for (int qt = 0; qt < QT; ++qt) AttnMfma<bf16_t>::run(kf, qf[qt][ks], s[qt][kt]);
+          for (int qt = 0; qt < QT; ++qt) AttnMfma<T>::run(kf, qf[qt][ks], s[qt][kt]);
         }
       }
       constexpr float kLazyLog2 = 8.0f;
@@ -599,17 +600,17 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4,
         u32x4_t pf[QT];
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt)
-          pf[qt] = u32x4_t{pack_bf16x2(s[qt][2 * c][0], s[qt][2 * c][1]),
-                           pack_bf16x2(s[qt][2 * c][2], s[qt][2 * c][3]),
-                           pack_bf16x2(s[qt][2 * c + 1][0], s[qt][2 * c + 1][1]),
-                           pack_bf16x2(s[qt][2 * c + 1][2], s[qt][2 * c + 1][3])};
+          pf[qt] = u32x4_t{pack2<T>(s[qt][2 * c][0], s[qt][2 * c][1]),
+                           pack2<T>(s[qt][2 * c][2], s[qt][2 * c][3]),
+                           pack2<T>(s[qt][2 * c + 1][0], s[qt][2 * c + 1][1]),
+                           pack2<T>(s[qt][2 * c + 1][2], s[qt][2 * c + 1][3])};
 #pragma unroll
         for (int dt = 0; dt < ND; ++dt) {
           const u32x2_t lo = vt_read(sv, 32 * c + tr_row, dt);
           const u32x2_t hi = vt_read(sv, 32 * c + 16 + tr_row, dt);
           const u32x4_t vf = {lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
-          for (int qt = 0; qt < QT; ++qt) AttnMfma<bf16_t>::run(vf, pf[qt], o_acc[qt][dt]);
+          for (int qt = 0; qt < QT; ++qt) AttnMfma<T>::run(vf, pf[qt], o_acc[qt][dt]);
         }
       }
     }
@@ -623,7 +624,7 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4,
     l = column_sum(l);
     if (qi >= Tq) continue;
     const float inv = l > 0.f ? 1.0f / l : 0.f;
-    bf16_t* orow = O + b * o_sb + h * o_sh + qi * o_st;
+    T* orow = O + b * o_sb + h * o_sh + qi * o_st;
 #pragma unroll
     for (int dt = 0; dt < ND; ++dt) {
       float v[4];
@@ -648,7 +649,7 @@ static bool attn_dma_ok(int Tk, const int64_t* st) {
 // (bit-identical outputs): 8x12x512 216 -> 263 TFLOP/s, 16x8x256 126 -> 154,
 // GPT-2 XL prefill 32x25x128 107 -> 118; at 16x12x1024 (6 blocks per CU) 64
 // queries fell from 542 to 454.
-template <int HD, int STAGES, int QTW>
+template <int HD, int STAGES, int QTW, typename T>
 static int launch_attn_dma_qt(const void* q, const void* k, const void* v, void* o, int B, int H,
                               int Tq, int Tk, const int64_t* st, float scale, int causal,
                               hipStream_t s) {
@@ -658,10 +659,9 @@ static int launch_attn_dma_qt(const void* q, const void* k, const void* v, void*
   const int64_t blocks = static_cast<int64_t>(n_bh) * n_qblk;
   if (blocks > 0x7fffffff) return CGPT_ESHAPE;
   const float scale_log2 = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL((attn_fwd_dma_kernel<HD, STAGES, QTW>), dim3(static_cast<unsigned>(blocks)),
-                     dim3(kAttnThreads), 0, s, static_cast<const bf16_t*>(q),
-                     static_cast<const bf16_t*>(k), static_cast<const bf16_t*>(v),
-                     static_cast<bf16_t*>(o), H, Tq, Tk, st[0], st[1], st[2], st[3], st[4], st[5],
+  hipLaunchKernelGGL((attn_fwd_dma_kernel<HD, STAGES, QTW, T>), dim3(static_cast<unsigned>(blocks)),
+                     dim3(kAttnThreads), 0, s, static_cast<const T*>(q), static_cast<const T*>(k),
+                     static_cast<const T*>(v), static_cast<T*>(o), H, Tq, Tk, st[0], st[1], st[2], st[3], st[4], st[5],
                      st[6], st[7], st[8], st[9], st[10], st[11], scale_log2, causal, n_bh);
   return hip_status(hipGetLastError());
 }
@@ -674,22 +674,22 @@ static int attn_num_cus() {
   return n;
 }
 
-template <int HD, int STAGES>
+template <int HD, int STAGES, typename T>
 static int launch_attn_dma(const void* q, const void* k, const void* v, void* o, int B, int H,
                            int Tq, int Tk, const int64_t* st, float scale, int causal,
                            hipStream_t s) {
   const int64_t blocks128 = static_cast<int64_t>(B) * H * ((Tq + 127) / 128);
   if (blocks128 < 4 * static_cast<int64_t>(attn_num_cus()))
-    return launch_attn_dma_qt<HD, STAGES, 1>(q, k, v, o, B, H, Tq, Tk, st, scale, causal, s);
-  return launch_attn_dma_qt<HD, STAGES, 2>(q, k, v, o, B, H, Tq, Tk, st, scale, causal, s);
+    return launch_attn_dma_qt<HD, STAGES, 1, T>(q, k, v, o, B, H, Tq, Tk, st, scale, causal, s);
+  return launch_attn_dma_qt<HD, STAGES, 2, T>(q, k, v, o, B, H, Tq, Tk, st, scale, causal, s);
 }
 
 template <typename T, int HD>
 static int launch_attn(const void* q, const void* k, const void* v, void* o, int B, int H, int Tq,
                        int Tk, const int64_t* st, float scale, int causal, hipStream_t s) {
-  if constexpr (std::is_same<T, bf16_t>::value && (HD == 64 || HD == 128)) {
+  if constexpr (sizeof(T) == 2 && (HD == 64 || HD == 128)) {
     if (attn_dma_ok(Tk, st))
-      return launch_attn_dma<HD, 2>(q, k, v, o, B, H, Tq, Tk, st, scale, causal, s);
+      return launch_attn_dma<HD, 2, T>(q, k, v, o, B, H, Tq, Tk, st, scale, causal, s);
   }
   // 64-query blocks when 128-query ones would give fewer than four per CU, as
   // for the DMA kernel.

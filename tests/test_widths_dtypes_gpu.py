@@ -166,9 +166,11 @@ def test_layernorm_fp16(gpu, rows, cols, with_delta):
         close(xo, s, 1e-7, 2 ** -11, "ln fp16 x_out")
 
 
-@pytest.mark.parametrize("hd,T", [(64, 200), (32, 64), (128, 300)])
-def test_attention_fp16(gpu, hd, T):
-    B, H = 2, 3
+@pytest.mark.parametrize("B,H,hd,T", [(2, 3, 64, 200), (2, 3, 32, 64), (2, 3, 128, 300),
+                                       (8, 16, 64, 1024)])
+def test_attention_fp16(gpu, B, H, hd, T):
+    """fp16 causal attention: the direct-to-LDS kernel (head_dim 64 / 128; 64-
+    and, at 8x16x1024, 128-query blocks) and the register-staged one (32)."""
     q, k, v = (randn(B, H, T, hd, seed=i, dtype=F16) for i in range(3))
     o = cg.cutile_causal_attention(q.to(gpu), k.to(gpu), v.to(gpu), H)
     assert o.dtype == F16
