@@ -51,6 +51,27 @@ __device__ __forceinline__ void store4_nt(bf16_t* p, const float* v) {
   __builtin_nontemporal_store(u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])},
                               reinterpret_cast<u32x2_t*>(p));
 }
+__device__ __forceinline__ void load4(const f16_t* p, float* v) {
+  const u32x2_t u = *reinterpret_cast<const u32x2_t*>(p);
+  v[0] = f16_lo(u[0]);
+  v[1] = f16_hi(u[0]);
+  v[2] = f16_lo(u[1]);
+  v[3] = f16_hi(u[1]);
+}
+__device__ __forceinline__ void store4(f16_t* p, const float* v) {
+  *reinterpret_cast<u32x2_t*>(p) = u32x2_t{pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])};
+}
+__device__ __forceinline__ void load4_nt(const f16_t* p, float* v) {
+  const u32x2_t u = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+  v[0] = f16_lo(u[0]);
+  v[1] = f16_hi(u[0]);
+  v[2] = f16_lo(u[1]);
+  v[3] = f16_hi(u[1]);
+}
+__device__ __forceinline__ void store4_nt(f16_t* p, const float* v) {
+  __builtin_nontemporal_store(u32x2_t{pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])},
+                              reinterpret_cast<u32x2_t*>(p));
+}
 template <bool NT, typename T> __device__ __forceinline__ void load4p(const T* p, float* v) {
   if constexpr (NT) load4_nt(p, v); else load4(p, v);
 }
@@ -61,12 +82,20 @@ template <bool NT, typename T> __device__ __forceinline__ void store4p(T* p, con
 // gamma / beta: 16 raw bytes from the chunk's first element through a buffer
 // resource (fp32: 4 values; bf16: the first 8 bytes), decoded by the uniform
 // type flag after the load, so no branch separates a load from its use.
+template <typename P16 = bf16_t>
 __device__ __forceinline__ void decode_param(u32x4_t r, bool bf16, float* v) {
   if (bf16) {
-    v[0] = __uint_as_float(r[0] << 16);
-    v[1] = __uint_as_float(r[0] & 0xffff0000u);
-    v[2] = __uint_as_float(r[1] << 16);
-    v[3] = __uint_as_float(r[1] & 0xffff0000u);
+    if constexpr (std::is_same<P16, f16_t>::value) {
+      v[0] = f16_lo(r[0]);
+      v[1] = f16_hi(r[0]);
+      v[2] = f16_lo(r[1]);
+      v[3] = f16_hi(r[1]);
+    } else {
+      v[0] = __uint_as_float(r[0] << 16);
+      v[1] = __uint_as_float(r[0] & 0xffff0000u);
+      v[2] = __uint_as_float(r[1] << 16);
+      v[3] = __uint_as_float(r[1] & 0xffff0000u);
+    }
   } else {
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[j] = __uint_as_float(r[j]);
@@ -150,8 +179,10 @@ __global__ __launch_bounds__(kLnThreads) void add_layernorm_kernel(
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     float gm[4], bt[4];
-    decode_param(graw[c], param_bf16, gm);
-    decode_param(braw[c], param_bf16, bt);
+    // 16-bit parameters have the type of an fp16 row, else bf16.
+    using P16 = typename std::conditional<std::is_same<TX, f16_t>::value, f16_t, bf16_t>::type;
+    decode_param<P16>(graw[c], param_bf16, gm);
+    decode_param<P16>(braw[c], param_bf16, bt);
     const int col = (c * 64 + lane) * 4;
 #pragma unroll
     for (int i = 0; i < R; ++i) {
@@ -685,6 +716,28 @@ extern "C" int cgpt_add_layernorm(const void* x, const void* delta, void* x_out,
                    ptr_aligned(x, x_dtype) && ptr_aligned(x_out, x_dtype) &&
                    ptr_aligned(y, y_dtype) && ptr_aligned(gamma, param_dtype) &&
                    ptr_aligned(beta, param_dtype) && (delta == nullptr || ptr_aligned(delta, delta_dtype));
+  // fp16 rows (x, delta, y all fp16; fp16 or fp32 parameters) on the same
+  // register-resident kernel, 8-byte aligned like bf16.
+  const bool vec16 = x_dtype == CGPT_F16 && y_dtype == CGPT_F16 &&
+                     (delta == nullptr || delta_dtype == CGPT_F16) &&
+                     (param_dtype == CGPT_F16 || param_dtype == CGPT_F32) && cols % 4 == 0 &&
+                     cols <= 4096 && aligned8(x) && (x_out == nullptr || aligned8(x_out)) &&
+                     aligned8(y) && (delta == nullptr || aligned8(delta)) &&
+                     ptr_aligned(gamma, param_dtype) && ptr_aligned(beta, param_dtype);
+  if (vec16) {
+    const f16_t* xp = static_cast<const f16_t*>(x);
+    const f16_t* dp = static_cast<const f16_t*>(delta);
+    f16_t* xo = static_cast<f16_t*>(x_out);
+    f16_t* yp = static_cast<f16_t*>(y);
+    const bool p16 = param_dtype == CGPT_F16;
+    if (dp != nullptr)
+      launch_ln_cols<f16_t, f16_t, f16_t, true>(xp, dp, xo, gamma, beta, p16, yp, rows,
+                                                static_cast<int>(cols), eps, s);
+    else
+      launch_ln_cols<f16_t, f16_t, f16_t, false>(xp, dp, xo, gamma, beta, p16, yp, rows,
+                                                 static_cast<int>(cols), eps, s);
+    return hip_status(hipGetLastError());
+  }
   if (!vec) {
     if (rows > 0x7fffffff) return CGPT_ESHAPE;
     hipLaunchKernelGGL(add_layernorm_any_kernel, dim3(static_cast<unsigned>(rows)), dim3(kLnThreads),

@@ -123,8 +123,9 @@ def cutile_layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor,
 
     Replaces ``cutile_layer_norm`` (``cutile_gpt/kernels/layernorm.py:77-135``)
     for rows of any width, without the reference's power-of-two padding copies:
-    float32 / bfloat16 rows of a multiple of 4 up to 4096 elements stay in
-    registers, other widths and float16 take a block-per-row kernel.
+    rows of a multiple of 4 up to 4096 elements stay in registers (float32,
+    bfloat16, or float16 throughout), other widths and dtype mixes take a
+    block-per-row kernel.
     """
     return add_layer_norm(x, None, weight, bias, eps)
 

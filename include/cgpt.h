@@ -70,9 +70,10 @@ int cgpt_gelu(const void* x, void* y, int64_t n, int dtype, void* stream);
  * Row r of x / delta / x_out / y starts at r * cols.  gamma and beta hold
  * `cols` elements of `param_dtype`.  Statistics are accumulated in fp32.
  * Any cols >= 1 and any dtype mix of CGPT_F32 / CGPT_BF16 / CGPT_F16 with
- * element-aligned pointers: fp32 / bf16 rows of cols % 4 == 0, cols <= 4096,
- * 16-byte (fp32) or 8-byte (bf16) aligned take the register-resident vector
- * kernels, the rest a block-per-row kernel (three passes over the row).
+ * element-aligned pointers: fp32 / bf16 rows (or all-fp16 rows with fp16 /
+ * fp32 gamma and beta) of cols % 4 == 0, cols <= 4096, 16-byte (fp32) or
+ * 8-byte (16-bit) aligned take the register-resident vector kernels, the rest
+ * a block-per-row kernel (three passes over the row).
  * Replaces cutile_layer_norm, cutile_gpt/kernels/layernorm.py:77-135 (kernel
  * :24-74), fused with the residual adds at cutile_gpt/models/gpt.py:155,174.
  */

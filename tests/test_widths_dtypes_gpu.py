@@ -149,13 +149,16 @@ def test_gelu_fp16(gpu, n):
     close(y, R.gelu_tanh(x.double()), 1e-6, 2 ** -11, "gelu fp16")
 
 
-@pytest.mark.parametrize("rows,cols", [(3, 48), (37, 768), (5, 1600), (2, 4100)])
+@pytest.mark.parametrize("rows,cols", [(3, 48), (37, 768), (5, 1600), (2, 4100), (16384, 768)])
 @pytest.mark.parametrize("with_delta", [False, True])
-def test_layernorm_fp16(gpu, rows, cols, with_delta):
+@pytest.mark.parametrize("pd", [F16, F32])
+def test_layernorm_fp16(gpu, rows, cols, with_delta, pd):
+    """fp16 rows: the register-resident kernel up to 4096 columns (fp16 or fp32
+    gamma / beta), the block-per-row kernel beyond."""
     x = randn(rows, cols, seed=rows, dtype=F16)
     d = randn(rows, cols, seed=cols, dtype=F16) if with_delta else None
-    g = (1 + 0.1 * randn(cols, seed=1)).to(F16)
-    b = (0.1 * randn(cols, seed=2)).to(F16)
+    g = (1 + 0.1 * randn(cols, seed=1)).to(pd)
+    b = (0.1 * randn(cols, seed=2)).to(pd)
     xg = x.to(gpu)
     xo = torch.empty_like(xg) if with_delta else None
     y = cg.add_layer_norm(xg, None if d is None else d.to(gpu), g.to(gpu), b.to(gpu), 1e-5,
