@@ -22,8 +22,9 @@
 //    key order inside one MFMA k-slab is permuted identically on both operands
 //    (lane group g, element i <-> key 4g + i of the first 16-key tile, then of
 //    the second), which leaves the contraction unchanged.
-//  * bf16: v_mfma_f32_16x16x32_bf16; P is rounded to bf16 before P.V while the
-//    normaliser accumulates the unrounded fp32 P.  fp32: v_mfma_f32_16x16x4_f32.
+//  * bf16 / fp16: v_mfma_f32_16x16x32_bf16 / _f16; P is rounded to the input
+//    type before P.V while the normaliser accumulates the unrounded fp32 P.
+//    fp32: v_mfma_f32_16x16x4_f32.
 //  * Softmax runs in the base-2 domain with scale * log2(e) folded into one
 //    multiply; fully masked rows never produce NaN (the running max is clamped
 //    to 0 while it is still -inf).
@@ -352,7 +353,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
   }
 }
 
-// bf16 variant with K and V streamed straight into LDS (head_dim 64 or 128).
+// 16-bit (bf16 / fp16) variant with K and V streamed straight into LDS
+// (head_dim 64 or 128).
 // Differences from attn_fwd_kernel:
 //  * Keys and values go global -> LDS by buffer_load ... lds (no staging
 //    registers, no LDS writes), STAGES blocks deep: block j + STAGES - 1 is

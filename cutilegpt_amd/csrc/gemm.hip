@@ -12,7 +12,8 @@
 //    "B" operand, so the 16x16 accumulator is C^T: lane l holds C[m = l%16]
 //    [n = 4(l/16) .. 4(l/16)+3] — four consecutive output columns of one row,
 //    which makes bias, GELU and the store 4-wide.
-//  * bf16: v_mfma_f32_16x16x32_bf16 (each lane supplies 8 consecutive k).
+//  * bf16 / fp16: v_mfma_f32_16x16x32_bf16 / _f16 (each lane supplies 8
+//    consecutive k); every 16-bit kernel is templated on the input type.
 //    fp32: four v_mfma_f32_16x16x4_f32 per 16-byte fragment; lane group g
 //    supplies k = 4g + j to the j-th MFMA (any consistent permutation of the
 //    k axis leaves the dot product unchanged).
@@ -20,11 +21,13 @@
 //    (GROUP_M) order run on the same XCD (the dispatcher deals block ids
 //    round-robin over the 8 XCDs, each with its own L2).
 //
-// Two main loops:
+// Main loops:
 //  * gemm_kernel: global -> registers -> LDS double buffering (fp32, and small
-//    bf16 problems, any K multiple of 8/4).
-//  * gemm_pipe_kernel: bf16 direct-to-LDS multi-stage pipeline, persistent
-//    over tiles (see the comment above it).
+//    16-bit problems, any K multiple of 8/4; with element loads, any K, stride
+//    or alignment).
+//  * gemm_pipe_kernel / gemm_pipe_a3_kernel / gemm_slab_kernel: 16-bit
+//    direct-to-LDS multi-stage pipelines, persistent over tiles (see the
+//    comments above them).
 #include "common.h"
 #include "gemm_common.h"
 #include "internal.h"
@@ -263,7 +266,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// bf16 direct-to-LDS pipeline, persistent over tiles.
+// 16-bit (bf16 / fp16) direct-to-LDS pipeline, persistent over tiles.
 //
 // * Tiles reach LDS through `buffer_load_dwordx4 ... lds`: each lane's 16 bytes
 //   land at (LDS base + lane * 16), so one wave instruction fills 1 KiB of LDS
@@ -1631,12 +1634,12 @@ static int auto_tile(bool half, int M, int N, int K, int64_t lda, int64_t ldw, i
 }
 
 // Residual epilogue (C += A W^T + bias).  `tile`: 14 = the slab kernel's
-// residual ring (bf16 inputs into fp32 C, at least 8 k64 steps, whole
+// residual ring (16-bit inputs into fp32 C, at least 8 k64 steps, whole
 // 4-column groups, 32-bit offsets; otherwise as TILE_AUTO); 17-19 = that
-// small pipeline tile (bf16, K % 64 == 0; otherwise as TILE_AUTO); a
+// small pipeline tile (16-bit inputs, K % 64 == 0; otherwise as TILE_AUTO); a
 // register-staged tile id (bf16 / fp16 0-4, fp32 0-1) = that tile; anything
 // else = TILE_AUTO: the slab kernel when its 256x192 tiles give at least half
-// the CUs a tile, else the 128x64 pipeline (bf16, K % 64 == 0), else the
+// the CUs a tile, else the 128x64 pipeline (16-bit inputs, K % 64 == 0), else the
 // register-staged tile the library's heuristic gives (the largest with 512
 // blocks, 64x64 below that).
 template <typename TIn, typename TOut>
