@@ -1376,6 +1376,23 @@ static int num_cus() {
   return cache[dev];
 }
 
+// Blocks for a persistent launch: one per tile, up to as many as fit on every
+// CU at once — registers and LDS, from the runtime's occupancy query for that
+// kernel, looked up on its first launch and kept in `occ`.  The 4-wave
+// pipeline tiles fit two (128x128, 128x64) or three (64x64) blocks a CU, whose
+// waves hide each other's memory waits (XL MLP c_proj with the residual add,
+// 4096 x 1600 x 6400, 128x128 tiles: 134 -> 91 us); the 8-wave kernels fit one.
+static int persistent_grid(const void* kernel, int threads, int64_t tiles, int& occ) {
+  if (occ == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) != hipSuccess || n < 1)
+      n = 1;
+    occ = n;
+  }
+  const int64_t cap = static_cast<int64_t>(occ) * num_cus();
+  return static_cast<int>(tiles < cap ? tiles : cap);
+}
+
 // WSO: 0 = buffer (or plain) stores, else the wave-staged output mode to use
 // where the output allows it (kOutWaveStaged or kOutWaveStagedNT).
 template <int BM, int BN, int WGM, int WGN, int SPS, int STAGES, int EPI, typename TOut,
@@ -1393,7 +1410,7 @@ static int launch_pipe(const void* a, const void* w, const void* bias, bool bias
   const int tiles_n = (N + BN - 1) / BN;
   const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
   if (tiles > 0x7fffffff) return CGPT_ESHAPE;
-  const int grid = static_cast<int>(tiles < num_cus() ? tiles : num_cus());
+  constexpr int kThreads = 64 * WGM * WGN;
   // Buffer-resource stores write whole 4-column groups and address one tile's
   // rows with 31-bit byte offsets; staged stores write whole 16-byte chunks.
   const bool buf_store = vec_store && N % 4 == 0 &&
@@ -1403,23 +1420,36 @@ static int launch_pipe(const void* a, const void* w, const void* bias, bool bias
                       reinterpret_cast<uintptr_t>(c) % 16 == 0;
   if constexpr (WSO != 0) {
     if (staged) {
+      static int occ = 0;
+      const int grid = persistent_grid(
+          reinterpret_cast<const void*>(&gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut, WSO, TIn>),
+          kThreads, tiles, occ);
       hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut, WSO, TIn>),
-                         dim3(grid), dim3(64 * WGM * WGN), 0, s, static_cast<const TIn*>(a),
+                         dim3(grid), dim3(kThreads), 0, s, static_cast<const TIn*>(a),
                          static_cast<const TIn*>(w), bias, bias_bf16, static_cast<TOut*>(c), M,
                          N, K, lda, ldw, ldc, tiles_m, tiles_n, vec_store);
       return hip_status(hipGetLastError());
     }
   }
-  if (buf_store)
+  if (buf_store) {
+    static int occ = 0;
+    const int grid = persistent_grid(
+        reinterpret_cast<const void*>(&gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut, kOutBuffer, TIn>),
+        kThreads, tiles, occ);
     hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut, kOutBuffer, TIn>), dim3(grid),
-                       dim3(64 * WGM * WGN), 0, s, static_cast<const TIn*>(a),
+                       dim3(kThreads), 0, s, static_cast<const TIn*>(a),
                        static_cast<const TIn*>(w), bias, bias_bf16, static_cast<TOut*>(c), M, N,
                        K, lda, ldw, ldc, tiles_m, tiles_n, vec_store);
-  else
+  } else {
+    static int occ = 0;
+    const int grid = persistent_grid(
+        reinterpret_cast<const void*>(&gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut, kOutPlain, TIn>),
+        kThreads, tiles, occ);
     hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut, kOutPlain, TIn>), dim3(grid),
-                       dim3(64 * WGM * WGN), 0, s, static_cast<const TIn*>(a),
+                       dim3(kThreads), 0, s, static_cast<const TIn*>(a),
                        static_cast<const TIn*>(w), bias, bias_bf16, static_cast<TOut*>(c), M, N,
                        K, lda, ldw, ldc, tiles_m, tiles_n, vec_store);
+  }
   return hip_status(hipGetLastError());
 }
 
@@ -1638,10 +1668,47 @@ static int auto_tile(bool half, int M, int N, int K, int64_t lda, int64_t ldw, i
 // 4-column groups, 32-bit offsets; otherwise as TILE_AUTO); 17-19 = that
 // small pipeline tile (16-bit inputs, K % 64 == 0; otherwise as TILE_AUTO); a
 // register-staged tile id (bf16 / fp16 0-4, fp32 0-1) = that tile; anything
-// else = TILE_AUTO: the slab kernel when its 256x192 tiles give at least half
-// the CUs a tile, else the 128x64 pipeline (16-bit inputs, K % 64 == 0), else the
+// else = TILE_AUTO: the slab kernel when its 256x192 tiles give every CU a
+// tile, else the largest 4-wave pipeline tile (128x128, 128x64, 64x64) with
+// at least 1.5 tiles a CU, else 64x64 (16-bit inputs, K % 64 == 0), else the
 // register-staged tile the library's heuristic gives (the largest with 512
 // blocks, 64x64 below that).
+template <typename TIn, int EPI, typename TOut>
+static int launch_small_pipe(int tile, const void* a, const void* w, const void* bias,
+                             bool bias_bf16, void* c, int M, int N, int K, int64_t lda,
+                             int64_t ldw, int64_t ldc, bool vec_store, hipStream_t s) {
+  switch (tile) {
+    case 17:
+      return launch_pipe<128, 128, 2, 2, 2, 2, EPI, TOut, 0, TIn>(a, w, bias, bias_bf16, c, M, N, K,
+                                                                  lda, ldw, ldc, vec_store, s);
+    case 18:
+      return launch_pipe<128, 64, 2, 2, 2, 3, EPI, TOut, 0, TIn>(a, w, bias, bias_bf16, c, M, N, K,
+                                                                 lda, ldw, ldc, vec_store, s);
+    default:
+      return launch_pipe<64, 64, 2, 2, 2, 3, EPI, TOut, 0, TIn>(a, w, bias, bias_bf16, c, M, N, K,
+                                                                lda, ldw, ldc, vec_store, s);
+  }
+}
+
+// The largest 4-wave pipeline tile that gives the CUs at least 1.5 tiles each
+// (their blocks run two or three a CU), else 64x64; -1 when K or the offsets
+// rule the pipeline out.  Residual projections measured with each: XL
+// 4096 x 1600 x 6400 128x128 91 / 128x64 112 / 64x64 138 us, 4096 x 1600 x
+// 1600 33 / 38 / 41 us (the slab's 144 tiles: 123 and 43 us); medium
+// 4096 x 512 x 2048 26 / 20 / 17 us.
+static int small_pipe_tile(int M, int N, int K, int64_t lda, int64_t ldw) {
+  constexpr int kIds[3] = {17, 18, 19}, kBm[3] = {128, 128, 64}, kBn[3] = {128, 64, 64};
+  const int64_t cus = num_cus();
+  int fallback = -1;
+  for (int i = 0; i < 3; ++i) {
+    if (!pipe_ok(kIds[i], M, N, K, lda, ldw)) continue;
+    const int64_t t = static_cast<int64_t>((M + kBm[i] - 1) / kBm[i]) * ((N + kBn[i] - 1) / kBn[i]);
+    if (2 * t >= 3 * cus) return kIds[i];
+    fallback = kIds[i];
+  }
+  return fallback;
+}
+
 template <typename TIn, typename TOut>
 static int launch_resid(int req_tile, const void* a, const void* w, const void* bias,
                         bool bias_bf16, void* c, int M, int N, int K, int64_t lda, int64_t ldw,
@@ -1651,25 +1718,15 @@ static int launch_resid(int req_tile, const void* a, const void* w, const void* 
   const bool reg_tile = req_tile >= 0 && req_tile <= last;
   if constexpr (sizeof(TIn) == 2) {
     if (req_tile >= kFirstSmallPipeTile && req_tile < kNumBf16Tiles &&
-        pipe_ok(req_tile, M, N, K, lda, ldw)) {
-      switch (req_tile) {
-        case 17:
-          return launch_pipe<128, 128, 2, 2, 2, 2, EPI, TOut, 0, TIn>(a, w, bias, bias_bf16, c, M, N,
-                                                                      K, lda, ldw, ldc, vec_store, s);
-        case 18:
-          return launch_pipe<128, 64, 2, 2, 2, 3, EPI, TOut, 0, TIn>(a, w, bias, bias_bf16, c, M, N,
-                                                                     K, lda, ldw, ldc, vec_store, s);
-        default:
-          return launch_pipe<64, 64, 2, 2, 2, 3, EPI, TOut, 0, TIn>(a, w, bias, bias_bf16, c, M, N,
-                                                                    K, lda, ldw, ldc, vec_store, s);
-      }
-    }
+        pipe_ok(req_tile, M, N, K, lda, ldw))
+      return launch_small_pipe<TIn, EPI, TOut>(req_tile, a, w, bias, bias_bf16, c, M, N, K, lda,
+                                               ldw, ldc, vec_store, s);
   }
   if constexpr (sizeof(TIn) == 2 && sizeof(TOut) == 4) {
     const int64_t m = M, n = N;
     const int tiles_m = (M + 255) / 256, tiles_n = (N + 191) / 192;
     const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
-    const bool want = req_tile == 14 || (!reg_tile && 2 * tiles >= num_cus());
+    const bool want = req_tile == 14 || (!reg_tile && tiles >= num_cus());
     if (want && K % 64 == 0 && K / 64 >= kResidMinSteps && n % 4 == 0 && ldc % 4 == 0 &&
         reinterpret_cast<uintptr_t>(c) % 16 == 0 && (m + 256) * ldc * 4 < (int64_t{1} << 32) &&
         (m + 256) * lda * 2 < (int64_t{1} << 32) && (n + 192) * ldw * 2 < (int64_t{1} << 32) &&
@@ -1683,13 +1740,14 @@ static int launch_resid(int req_tile, const void* a, const void* w, const void* 
       return hip_status(hipGetLastError());
     }
   }
-  // Too few slab tiles for the CUs: the 128x64 pipeline (4 waves) where K
-  // allows it (medium's 4096x512 projections: 13.0 -> 8.7 and 29.2 -> 20.1
-  // us against the 64x64 register tile).
+  // Fewer slab tiles than CUs: a 4-wave pipeline tile where K allows it
+  // (medium's 4096x512 projections: 13.0 -> 7.8 and 29.2 -> 16.9 us against
+  // the 64x64 register tile).
   if constexpr (sizeof(TIn) == 2) {
-    if (!reg_tile && pipe_ok(18, M, N, K, lda, ldw))
-      return launch_pipe<128, 64, 2, 2, 2, 3, EPI, TOut, 0, TIn>(a, w, bias, bias_bf16, c, M, N, K,
-                                                                 lda, ldw, ldc, vec_store, s);
+    const int pick = reg_tile ? -1 : small_pipe_tile(M, N, K, lda, ldw);
+    if (pick >= 0)
+      return launch_small_pipe<TIn, EPI, TOut>(pick, a, w, bias, bias_bf16, c, M, N, K, lda, ldw,
+                                               ldc, vec_store, s);
   }
   const TileCfg* t = sizeof(TIn) == 2 ? kBf16Tiles : kF32Tiles;
   const int first = sizeof(TIn) == 2 ? (K >= 2048 ? 2 : 3) : 0;

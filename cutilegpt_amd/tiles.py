@@ -31,7 +31,8 @@ Tile ids index the configuration table compiled into libcgpt.so
           16 = the same with non-temporal stores (the LM heads' fp32 logits,
                c_fc + GELU)
     bf16, the 2-3 stage pipeline with 4 waves on small tiles (also with the
-    residual epilogue; problems whose 256x192 tiles would leave most CUs idle):
+    residual epilogue; problems whose 256x192 tiles would leave CUs idle),
+    launched with as many blocks as fit a CU (two, or three at 64x64):
           17 = 128x128 (2 stages)  18 = 128x64 (3 stages)  19 = 64x64 (3 stages)
     fp32: 0 = 128x128, 1 = 64x64
 
@@ -72,15 +73,15 @@ TABLE: Dict[Tuple[int, int, int, int], int] = {
     (_B, 16384, 50304, 768): 16,  # lm head (vocab padded), fp32 out  991
     # 'medium' (8 layers, d 512) prefill, M = 16 x 256
     (_B, 4096, 1536, 512): 14,    # c_attn        463
-    (_B, 4096, 512, 512): 18,     # attn c_proj   243 (128x64 pipeline; 64x64 register 162, slab 102)
-    (_B, 4096, 2048, 512): 10,    # c_fc + GELU   520
-    (_B, 4096, 512, 2048): 18,    # mlp c_proj    427 (64x64 register 292, slab 183)
+    (_B, 4096, 512, 512): 19,     # attn c_proj   247 (64x64 pipeline; 128x64 221, 64x64 register 154)
+    (_B, 4096, 2048, 512): 17,    # c_fc + GELU   547 (128x256 pipeline 505)
+    (_B, 4096, 512, 2048): 19,    # mlp c_proj    480 (128x64 pipeline 413, 64x64 register 285)
     (_B, 4096, 50304, 512): 16,   # lm head       801
     # GPT-2 XL (48 layers, d 1600) prefill inside generate, M = 32 x 128
     (_B, 4096, 4800, 1600): 14,   # c_attn        961
-    (_B, 4096, 1600, 1600): 14,   # attn c_proj   479
-    (_B, 4096, 6400, 1600): 16,   # c_fc + GELU   929
-    (_B, 4096, 1600, 6400): 14,   # mlp c_proj    658
+    (_B, 4096, 1600, 1600): 17,   # attn c_proj   624 (slab 478: 144 tiles)
+    (_B, 4096, 6400, 1600): 17,   # c_fc + GELU   930 (256x256 919)
+    (_B, 4096, 1600, 6400): 17,   # mlp c_proj    913 (slab 663)
     (_B, 4096, 50304, 1600): 16,  # lm head      1076
 }
 

@@ -150,7 +150,7 @@ def test_tile_table_lookup():
     bf = _lib.CGPT_BF16
     assert tiles.gemm_tile(bf, 16384, 2304, 768) == tiles.gemm_tile(bf, 8200, 2304, 768) == 14
     assert tiles.gemm_tile(bf, 8192, 2304, 768) == _lib.TILE_AUTO
-    assert tiles.gemm_tile(bf, 3000, 512, 512) == 18
+    assert tiles.gemm_tile(bf, 3000, 512, 512) == 19
 
 
 def test_sampling_semantics_temperature_and_top_k():
