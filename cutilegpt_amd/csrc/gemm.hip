@@ -1614,6 +1614,25 @@ static int launch_tile(int tile, const void* a, const void* w, const void* bias,
 #undef CGPT_GEMM_CASE
 }
 
+// The largest 4-wave pipeline tile that gives the CUs at least 1.5 tiles each
+// (their blocks run two or three a CU), else 64x64; -1 when K or the offsets
+// rule the pipeline out.  Residual projections measured with each: XL
+// 4096 x 1600 x 6400 128x128 91 / 128x64 112 / 64x64 138 us, 4096 x 1600 x
+// 1600 33 / 38 / 41 us (the slab's 144 tiles: 123 and 43 us); medium
+// 4096 x 512 x 2048 26 / 20 / 17 us.
+static int small_pipe_tile(int M, int N, int K, int64_t lda, int64_t ldw) {
+  constexpr int kIds[3] = {17, 18, 19}, kBm[3] = {128, 128, 64}, kBn[3] = {128, 64, 64};
+  const int64_t cus = num_cus();
+  int fallback = -1;
+  for (int i = 0; i < 3; ++i) {
+    if (!pipe_ok(kIds[i], M, N, K, lda, ldw)) continue;
+    const int64_t t = static_cast<int64_t>((M + kBm[i] - 1) / kBm[i]) * ((N + kBn[i] - 1) / kBn[i]);
+    if (2 * t >= 3 * cus) return kIds[i];
+    fallback = kIds[i];
+  }
+  return fallback;
+}
+
 // Default tile choice when the caller's table has no entry: the register-staged
 // kernel with the largest tile that still gives every CU about two blocks
 // (128x128 for long K, 128x64 otherwise), smaller tiles for small grids.
@@ -1621,11 +1640,12 @@ static int auto_tile(bool half, int M, int N, int K, int64_t lda, int64_t ldw, i
   // 16-bit (bf16 / fp16) problems with at least one 256x192 tile per CU: the persistent
   // direct-to-LDS pipelines — 256x256 with wave-staged non-temporal stores
   // for wide N (the LM heads) and for the GELU epilogue; 256x192 with
-  // block-staged stores otherwise.  With fewer
-  // tiles than CUs, the persistent 256x192, 256x128 or 128x256 tile whose
-  // last round leaves the fewest CUs idle (ties to the larger tile), as long
-  // as it still gives half the CUs a tile; below that the register-staged
-  // kernel with smaller tiles.
+  // block-staged stores otherwise.  With fewer tiles than CUs, a 4-wave
+  // pipeline tile (several blocks a CU; medium's 4096 x 2048 x 512 c_fc:
+  // 15.7 us against 17.3 for 256x128), else the persistent 256x192, 256x128
+  // or 128x256 tile whose last round leaves the fewest CUs idle (ties to the
+  // larger tile), as long as it still gives half the CUs a tile; below that
+  // the register-staged kernel with smaller tiles.
   if (half) {
     auto tiles = [&](int bm, int bn) {
       return static_cast<int64_t>((M + bm - 1) / bm) * ((N + bn - 1) / bn);
@@ -1636,6 +1656,8 @@ static int auto_tile(bool half, int M, int N, int K, int64_t lda, int64_t ldw, i
       const int pick = (N >= 16384 || epi == CGPT_EPI_BIAS_GELU) ? 16 : 14;
       if (pipe_ok(pick, M, N, K, lda, ldw)) return pick;
     } else {
+      const int small = small_pipe_tile(M, N, K, lda, ldw);
+      if (small >= 0) return small;
       const int64_t cand_t[3] = {t14, tiles(256, 128), tiles(128, 256)};
       const int cand_id[3] = {14, 9, 10};
       int best = -1;
@@ -1688,25 +1710,6 @@ static int launch_small_pipe(int tile, const void* a, const void* w, const void*
       return launch_pipe<64, 64, 2, 2, 2, 3, EPI, TOut, 0, TIn>(a, w, bias, bias_bf16, c, M, N, K,
                                                                 lda, ldw, ldc, vec_store, s);
   }
-}
-
-// The largest 4-wave pipeline tile that gives the CUs at least 1.5 tiles each
-// (their blocks run two or three a CU), else 64x64; -1 when K or the offsets
-// rule the pipeline out.  Residual projections measured with each: XL
-// 4096 x 1600 x 6400 128x128 91 / 128x64 112 / 64x64 138 us, 4096 x 1600 x
-// 1600 33 / 38 / 41 us (the slab's 144 tiles: 123 and 43 us); medium
-// 4096 x 512 x 2048 26 / 20 / 17 us.
-static int small_pipe_tile(int M, int N, int K, int64_t lda, int64_t ldw) {
-  constexpr int kIds[3] = {17, 18, 19}, kBm[3] = {128, 128, 64}, kBn[3] = {128, 64, 64};
-  const int64_t cus = num_cus();
-  int fallback = -1;
-  for (int i = 0; i < 3; ++i) {
-    if (!pipe_ok(kIds[i], M, N, K, lda, ldw)) continue;
-    const int64_t t = static_cast<int64_t>((M + kBm[i] - 1) / kBm[i]) * ((N + kBn[i] - 1) / kBn[i]);
-    if (2 * t >= 3 * cus) return kIds[i];
-    fallback = kIds[i];
-  }
-  return fallback;
 }
 
 template <typename TIn, typename TOut>
