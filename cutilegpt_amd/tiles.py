@@ -61,28 +61,28 @@ def m_bucket(m: int) -> int:
     return 1 << max(0, (int(m) - 1).bit_length())
 
 
-# (dtype code, M bucket, N, K) -> tile id, from the sweep (TFLOP/s of the
+# (dtype code, M bucket, N, K) -> tile id, from the sweep (TFLOP/s by kernel time of the
 # winner, inputs hot; attn/MLP c_proj with the residual epilogue, fp32 out).
 _B = _lib.CGPT_BF16
 TABLE: Dict[Tuple[int, int, int, int], int] = {
     # GPT-2 124M prefill, M = 16 x 1024
-    (_B, 16384, 2304, 768): 14,   # c_attn        988
-    (_B, 16384, 768, 768): 14,    # attn c_proj   616 (register tiles <= 303)
-    (_B, 16384, 3072, 768): 16,   # c_fc + GELU   976
-    (_B, 16384, 768, 3072): 14,   # mlp c_proj   1002
-    (_B, 16384, 50304, 768): 16,  # lm head (vocab padded), fp32 out  991
+    (_B, 16384, 2304, 768): 14,   # c_attn       1075
+    (_B, 16384, 768, 768): 14,    # attn c_proj   636
+    (_B, 16384, 3072, 768): 16,   # c_fc + GELU  1074
+    (_B, 16384, 768, 3072): 14,   # mlp c_proj   1056
+    (_B, 16384, 50304, 768): 16,  # lm head (vocab padded), fp32 out  1015
     # 'medium' (8 layers, d 512) prefill, M = 16 x 256
-    (_B, 4096, 1536, 512): 14,    # c_attn        463
-    (_B, 4096, 512, 512): 19,     # attn c_proj   247 (64x64 pipeline; 128x64 221, 64x64 register 154)
-    (_B, 4096, 2048, 512): 17,    # c_fc + GELU   547 (128x256 pipeline 505)
-    (_B, 4096, 512, 2048): 19,    # mlp c_proj    480 (128x64 pipeline 413, 64x64 register 285)
-    (_B, 4096, 50304, 512): 16,   # lm head       801
+    (_B, 4096, 1536, 512): 14,    # c_attn        474
+    (_B, 4096, 512, 512): 19,     # attn c_proj   266 (64x64 pipeline)
+    (_B, 4096, 2048, 512): 17,    # c_fc + GELU   580 (128x128 pipeline)
+    (_B, 4096, 512, 2048): 19,    # mlp c_proj    497 (64x64 pipeline)
+    (_B, 4096, 50304, 512): 16,   # lm head       877
     # GPT-2 XL (48 layers, d 1600) prefill inside generate, M = 32 x 128
-    (_B, 4096, 4800, 1600): 14,   # c_attn        961
-    (_B, 4096, 1600, 1600): 17,   # attn c_proj   624 (slab 478: 144 tiles)
-    (_B, 4096, 6400, 1600): 17,   # c_fc + GELU   930 (256x256 919)
-    (_B, 4096, 1600, 6400): 17,   # mlp c_proj    913 (slab 663)
-    (_B, 4096, 50304, 1600): 16,  # lm head      1076
+    (_B, 4096, 4800, 1600): 14,   # c_attn       1015
+    (_B, 4096, 1600, 1600): 17,   # attn c_proj   661 (128x128 pipeline; slab: 144 tiles)
+    (_B, 4096, 6400, 1600): 16,   # c_fc + GELU   997 (128x128 pipeline 968)
+    (_B, 4096, 1600, 6400): 17,   # mlp c_proj    934 (128x128 pipeline)
+    (_B, 4096, 50304, 1600): 16,  # lm head      1156
 }
 
 
