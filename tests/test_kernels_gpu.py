@@ -561,12 +561,15 @@ def test_gemm_residual_epilogue_tiles(gpu, tile, m, n, k):
 
 @pytest.mark.parametrize("tile", [17, 18, 19])
 @pytest.mark.parametrize("m,n,k,ct", [(4096, 512, 2048, F32), (4096, 1600, 1600, F32),
+                                      (8192, 1600, 768, F32),
                                       (300, 520, 512, F32), (513, 200, 640, F32),
                                       (1000, 96, 128, BF16), (130, 102, 64, F32)])
 def test_gemm_residual_epilogue_small_pipeline_tiles(gpu, tile, m, n, k, ct):
     """The residual epilogue on the 4-wave persistent pipeline tiles (the old C
     values of a tile loaded before its stores; N % 4 != 0 takes per-element
-    stores): against the fp64 sum."""
+    stores): against the fp64 sum.  These kernels launch two or three blocks a
+    CU; 8192 x 1600 gives every tile size more tiles than such a grid, so
+    blocks walk one or two (128x128) up to five (64x64) tiles."""
     g = torch.Generator(device=gpu).manual_seed(m + 3 * n + k + tile)
     a = torch.randn(m, k, device=gpu, generator=g).to(BF16)
     w = (torch.randn(n, k, device=gpu, generator=g) * 0.05).to(BF16)
