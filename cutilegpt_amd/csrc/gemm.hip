@@ -28,6 +28,8 @@
 //  * gemm_pipe_kernel / gemm_pipe_a3_kernel / gemm_slab_kernel: 16-bit
 //    direct-to-LDS multi-stage pipelines, persistent over tiles (see the
 //    comments above them).
+#include <atomic>
+
 #include "common.h"
 #include "gemm_common.h"
 #include "internal.h"
@@ -1364,16 +1366,16 @@ static int launch_cfg(const void* a, const void* w, const void* bias, bool bias_
 // Compute units of the current device (persistent grids launch one block per
 // CU).  Cached per device id; concurrent first calls store the same value.
 static int num_cus() {
-  static int cache[64] = {0};
+  static std::atomic<int> cache[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int n = 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
       n = 256;
-    cache[dev] = n;
+    cache[dev].store(n, std::memory_order_relaxed);
   }
-  return cache[dev];
+  return n;
 }
 
 // Blocks for a persistent launch: one per tile, up to as many as fit on every
@@ -1382,14 +1384,14 @@ static int num_cus() {
 // pipeline tiles fit two (128x128, 128x64) or three (64x64) blocks a CU, whose
 // waves hide each other's memory waits (XL MLP c_proj with the residual add,
 // 4096 x 1600 x 6400, 128x128 tiles: 134 -> 91 us); the 8-wave kernels fit one.
-static int persistent_grid(const void* kernel, int threads, int64_t tiles, int& occ) {
-  if (occ == 0) {
-    int n = 0;
+static int persistent_grid(const void* kernel, int threads, int64_t tiles, std::atomic<int>& occ) {
+  int n = occ.load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) != hipSuccess || n < 1)
       n = 1;
-    occ = n;
+    occ.store(n, std::memory_order_relaxed);
   }
-  const int64_t cap = static_cast<int64_t>(occ) * num_cus();
+  const int64_t cap = static_cast<int64_t>(n) * num_cus();
   return static_cast<int>(tiles < cap ? tiles : cap);
 }
 
@@ -1420,7 +1422,7 @@ static int launch_pipe(const void* a, const void* w, const void* bias, bool bias
                       reinterpret_cast<uintptr_t>(c) % 16 == 0;
   if constexpr (WSO != 0) {
     if (staged) {
-      static int occ = 0;
+      static std::atomic<int> occ{0};
       const int grid = persistent_grid(
           reinterpret_cast<const void*>(&gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut, WSO, TIn>),
           kThreads, tiles, occ);
@@ -1432,7 +1434,7 @@ static int launch_pipe(const void* a, const void* w, const void* bias, bool bias
     }
   }
   if (buf_store) {
-    static int occ = 0;
+    static std::atomic<int> occ{0};
     const int grid = persistent_grid(
         reinterpret_cast<const void*>(&gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut, kOutBuffer, TIn>),
         kThreads, tiles, occ);
@@ -1441,7 +1443,7 @@ static int launch_pipe(const void* a, const void* w, const void* bias, bool bias
                        static_cast<const TIn*>(w), bias, bias_bf16, static_cast<TOut*>(c), M, N,
                        K, lda, ldw, ldc, tiles_m, tiles_n, vec_store);
   } else {
-    static int occ = 0;
+    static std::atomic<int> occ{0};
     const int grid = persistent_grid(
         reinterpret_cast<const void*>(&gemm_pipe_kernel<BM, BN, WGM, WGN, SPS, STAGES, EPI, TOut, kOutPlain, TIn>),
         kThreads, tiles, occ);
