@@ -289,7 +289,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(
 //   the same wait retires this step's LDS reads before the buffer is refilled.
 // * Persistent: block b walks tiles b, b + grid, ...; their K stages form one
 //   flattened stream, so the first stages of tile i+1 are in flight while tile
-//   i finishes.  The bias of the current tile is reloaded at every step before
+//   i finishes.  The grid holds as many blocks per CU as fit (one for the
+//   8-wave tiles, two or three for the 4-wave ones).  The bias of the current tile is reloaded at every step before
 //   the DMA (so it is older than anything a wait counts); the epilogue ends a
 //   tile's last step.  With buffer-resource stores an epilogue issues exactly
 //   TM * TN stores per wave and the following wait leaves them in flight;
@@ -1363,8 +1364,9 @@ static int launch_cfg(const void* a, const void* w, const void* bias, bool bias_
   return hip_status(hipGetLastError());
 }
 
-// Compute units of the current device (persistent grids launch one block per
-// CU).  Cached per device id; concurrent first calls store the same value.
+// Compute units of the current device (persistent grids launch as many blocks
+// per CU as fit).  Cached per device id; concurrent first calls store the same
+// value.
 static int num_cus() {
   static std::atomic<int> cache[64] = {};
   int dev = 0;
