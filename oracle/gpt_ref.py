@@ -349,3 +349,30 @@ def init_weights(n_layer: int, n_head: int, n_embd: int, vocab_size: int = 50257
     w["ln_f.bias"] = torch.zeros(D, dtype=dtype)
     w["lm_head.weight"] = w["wte"]
     return w
+
+
+AFFINE_KEYS = ("ln_1.weight", "ln_1.bias", "attn.c_attn.bias", "attn.c_proj.bias",
+               "ln_2.weight", "ln_2.bias", "mlp.c_fc.bias", "mlp.c_proj.bias")
+
+
+def randomize_affine(w: Dict[str, torch.Tensor], seed: int, std: float = 0.1) -> Dict[str, torch.Tensor]:
+    """A copy of ``w`` whose every bias and LayerNorm beta is ~N(0, std) and
+    every LayerNorm gamma ~N(1, std), as a trained checkpoint has them (the
+    reference's loader maps each of these tensors, ``models/gpt.py:266-296``,
+    and the forward uses each at its own place, ``:120-177``).
+
+    Every tensor is drawn separately, in the fixed order layer by layer over
+    ``AFFINE_KEYS`` and then ``ln_f``, from ``torch.Generator().manual_seed(seed)``
+    in fp32 and cast to the dtype it replaces, so two tensors of one shape
+    differ and a swap of any two changes the forward.  Matrices, embeddings and
+    a tied ``lm_head.weight`` are shared with ``w``."""
+    g = torch.Generator().manual_seed(seed)
+    out = dict(w)
+    names = [f"h.{i}.{k}" for i in range(_n_layer(w)) for k in AFFINE_KEYS]
+    for key in names + ["ln_f.weight", "ln_f.bias"]:
+        ref = w[key]
+        t = torch.randn(ref.shape, generator=g, dtype=torch.float32) * std
+        if key.endswith(("ln_1.weight", "ln_2.weight", "ln_f.weight")):
+            t = t + 1.0
+        out[key] = t.to(ref.dtype)
+    return out

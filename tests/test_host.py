@@ -122,7 +122,8 @@ def test_hf_checkpoint_roundtrip_and_transformers_agree(tmp_path):
     from transformers import GPT2LMHeadModel
 
     cfg = GPTConfig(n_layer=2, n_head=2, n_embd=32, block_size=64, vocab_size=50257)
-    w = R.init_weights(2, 2, 32, block_size=64, seed=11)
+    # every bias and LayerNorm tensor distinct, as in a trained checkpoint
+    w = R.randomize_affine(R.init_weights(2, 2, 32, block_size=64, seed=11), seed=12)
     save_hf_checkpoint(str(tmp_path), w, cfg)
     w2, cfg2 = load_hf_checkpoint(str(tmp_path))
     assert cfg2 == cfg
@@ -135,6 +136,12 @@ def test_hf_checkpoint_roundtrip_and_transformers_agree(tmp_path):
         ref = m(ids).logits
     out = R.gpt_forward(w2, ids, 2, R.FLOWS["fp32"])
     assert (out - ref).abs().max().item() < 1e-5
+    # transformers reads each bias / LayerNorm tensor from the key it was written to
+    sd = m.state_dict()
+    for i in range(2):
+        for name in ("ln_1.weight", "ln_1.bias", "attn.c_attn.bias", "attn.c_proj.bias",
+                     "ln_2.weight", "ln_2.bias", "mlp.c_fc.bias", "mlp.c_proj.bias"):
+            assert torch.equal(sd[f"transformer.h.{i}.{name}"], w[f"h.{i}.{name}"]), (i, name)
 
 
 def test_tile_table_lookup():

@@ -15,26 +15,9 @@ import torch
 from cutilegpt_amd import CutileGPT, GPTConfig, HFWeightLoader
 from cutilegpt_amd.hf_loader import internal_to_hf, save_hf_checkpoint
 from oracle import gpt_ref as R
+from tests.mingpt_stub import MinGPTStub
 
 pytestmark = pytest.mark.gpu
-
-
-class MinGPTStub(torch.nn.Module):
-    """Carries a minGPT state_dict: nn.Linear (out, in) weights under
-    ``transformer.*`` and a separate ``lm_head.weight`` (minGPT does not tie it)."""
-
-    def __init__(self, w, n_layer):
-        super().__init__()
-        self._sd = {"transformer.wte.weight": w["wte"], "transformer.wpe.weight": w["wpe"],
-                    "transformer.ln_f.weight": w["ln_f.weight"],
-                    "transformer.ln_f.bias": w["ln_f.bias"], "lm_head.weight": w["lm_head.weight"]}
-        for i in range(n_layer):
-            for k, v in w.items():
-                if k.startswith(f"h.{i}."):
-                    self._sd["transformer." + k] = v
-
-    def state_dict(self, *args, **kwargs):
-        return dict(self._sd)
 
 
 def untied_weights(n_layer, n_head, n_embd, seed, dtype=torch.float32):

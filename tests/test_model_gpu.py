@@ -3,21 +3,16 @@ and the golden fixture, at the benchmark configurations.
 
 Criteria (from the benchmark definition):
   fp32: max |logit error| <= 1e-3.
-  bf16: max |logit error| <= 3e-2 against the exact (fp64) forward and against
-        the oracle's bf16 flow (the HIP path's rounding points, fp32
-        arithmetic).  Top-1 agreement >= 99.9 % is not reachable between two
-        bf16 implementations of this model with random N(0, 0.02) weights: the
-        top-1/top-2 logit gap (~0.13) is within ~50x of the bf16 rounding
-        noise, so one flipped bf16 rounding anywhere upstream moves near-ties.
-        Measured on the CPU (medium config): the same bf16 flow in fp32 vs
-        fp64 arithmetic agrees on ~99.2 % of positions, and the three places
-        to round P in attention (two-pass, the reference's per-block online
-        rule, the kernel's lazy rescaling) agree pairwise on 98.4-98.9 %.
-        Asserted instead: top-1 agreement >= 98.5 % against both, 100 % at the
-        last position against fp64, every top-1 disagreement a near-tie (the
-        GPU's token scores within 3e-2 of the best under the oracle), and the
-        reference harness's ordered last-position top-5
-        (scripts/compare_mingpt.py:214-219) equal up to such near-ties.
+  bf16: ``tests/parity.check_bf16``: max |logit error| <= 3e-2 against the
+        exact (fp64) forward and against the oracle's bf16 flow (the HIP
+        path's rounding points), no larger than the reference's own bf16 flow
+        (``bf16_ref``) reaches against fp64, top-1 agreement at least that
+        flow's and above a floor set just under the measured figure (99.0 % at
+        GPT-2 and medium, 97.5 % at XL depth), every disagreement a near-tie.
+        Top-1 >= 99.9 % is not reachable between two bf16 implementations of
+        this model with random N(0, 0.02) weights: the reference's own bf16
+        flow agrees with fp64 on 96.9-97.5 % of positions here, the HIP flow
+        on 99.0-99.2 %.
 """
 
 import os
@@ -28,6 +23,7 @@ import torch
 
 from cutilegpt_amd import CutileGPT, GPTConfig
 from oracle import gpt_ref as R
+from tests.parity import NEAR_TIE, bf16_stats, check_bf16, report
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "nano_seed0.npz")
@@ -37,25 +33,6 @@ def make_model(cfg, w, dtype):
     m = CutileGPT(cfg, dtype=dtype, seed=0)
     m.load_weights(w)
     return m
-
-
-def agreement(a, b):
-    return (a.argmax(-1) == b.argmax(-1)).double().mean().item()
-
-
-def near_tie(out, ref):
-    """Largest ref.max - ref[argmax of out] over all positions: 0 where the
-    top-1 agrees, else how far the GPU's token is from the best under ref."""
-    a = out.argmax(-1, keepdim=True)
-    return (ref.amax(-1) - ref.gather(-1, a).squeeze(-1)).max().item()
-
-
-def top5_near_tie(out, ref):
-    """Largest |ref's r-th largest last-position logit - ref[out's r-th token]|
-    over ranks r < 5: 0 when the ordered top-5 lists are equal."""
-    idx = out[:, -1].topk(5, dim=-1).indices
-    vals = ref[:, -1].topk(5, dim=-1).values
-    return (vals - ref[:, -1].gather(-1, idx)).abs().max().item()
 
 
 def test_nano_fp32_vs_golden_and_oracle(gpu):
@@ -83,47 +60,13 @@ def test_nano_greedy_generate_matches_golden(gpu):
     assert np.array_equal(out.cpu().numpy(), gold["greedy_out"])
 
 
-def check_bf16(m, w, ids, n_head, label, rows=None):
-    logits, _ = m(ids.to(ids.device if ids.is_cuda else "cuda"))
-    out = logits.double().cpu()
-    sel = slice(None) if rows is None else rows
-    ids_cpu = ids.cpu()[sel]
-    out = out[sel]
-    exact = R.gpt_forward(w, ids_cpu, n_head, R.FLOWS["fp64"])
-    flow = R.gpt_forward(w, ids_cpu, n_head, R.FLOWS["bf16"]).double()
-    e_exact = (out - exact).abs().max().item()
-    e_flow = (out - flow).abs().max().item()
-    agree_all = agreement(out, exact)
-    agree_last = agreement(out[:, -1], exact[:, -1])
-    ref_agree = agreement(flow, exact)
-    agree_flow = agreement(out, flow)
-    # Reference harness (scripts/compare_mingpt.py:214-219): ordered top-5 at
-    # the last position of every sequence.
-    top5 = lambda t: t[:, -1].topk(5, dim=-1).indices
-    top5_exact = torch.equal(top5(out), top5(exact))
-    top5_flow = torch.equal(top5(out), top5(flow))
-    tie_flow, tie_exact = near_tie(out, flow), near_tie(out, exact)
-    t5_flow, t5_exact = top5_near_tie(out, flow), top5_near_tie(out, exact)
-    print(f"{label}: max|err| vs fp64 {e_exact:.3e}, vs bf16 flow {e_flow:.3e}; top-1 agree "
-          f"vs bf16 flow {agree_flow * 100:.3f}%, vs fp64 {agree_all * 100:.3f}% (oracle bf16 "
-          f"flow itself vs fp64 {ref_agree * 100:.3f}%), last pos {agree_last * 100:.1f}%; "
-          f"largest near-tie taken {tie_flow:.2e} (flow) / {tie_exact:.2e} (fp64); last-position "
-          f"top-5 equal to fp64 {top5_exact}, to bf16 flow {top5_flow} (largest rank gap "
-          f"{t5_exact:.2e} / {t5_flow:.2e})")
-    assert e_exact <= 3e-2 and e_flow <= 3e-2
-    assert agree_flow >= 0.985 and agree_all >= 0.985 and agree_last == 1.0
-    assert tie_flow <= 3e-2 and tie_exact <= 3e-2
-    assert t5_flow <= 3e-2 and t5_exact <= 3e-2
-    return agree_flow
-
-
 def test_medium_bf16(gpu):
     """'medium' GPT (8 layers, 8 heads, d 512), bf16 N(0,0.02) weights, b16 x s256."""
     cfg = GPTConfig(n_layer=8, n_head=8, n_embd=512, block_size=1024)
     w = R.init_weights(8, 8, 512, seed=0, dtype=torch.bfloat16)
     m = make_model(cfg, w, torch.bfloat16)
     ids = torch.randint(0, 50257, (16, 256), generator=torch.Generator().manual_seed(1))
-    check_bf16(m, w, ids, 8, "medium b16xs256")
+    check_bf16(m(ids.to(gpu))[0], w, ids, 8, "medium b16xs256", floor=0.99)
 
 
 def test_gpt2_bf16_full_batch(gpu):
@@ -133,7 +76,8 @@ def test_gpt2_bf16_full_batch(gpu):
     w = R.init_weights(12, 12, 768, seed=0, dtype=torch.bfloat16)
     m = make_model(cfg, w, torch.bfloat16)
     ids = torch.randint(0, 50257, (16, 1024), generator=torch.Generator().manual_seed(2))
-    check_bf16(m, w, ids, 12, "gpt2 b16xs1024 (rows 0 and 15)", rows=[0, 15])
+    check_bf16(m(ids.to(gpu))[0], w, ids, 12, "gpt2 b16xs1024 (rows 0 and 15)", rows=[0, 15],
+               floor=0.99)
 
 
 def test_gpt2_hf_checkpoint_load(gpu, tmp_path):
@@ -166,8 +110,8 @@ def test_ragged_lengths_fp32(gpu):
 
 def test_xl_bf16_prefill_all_positions(gpu):
     """GPT-2 XL depth (48 layers, 25 heads, d 1600), the XL workload's b32 x 128
-    prompts in bf16: every position of rows 0 and 1 against the fp64 oracle and
-    the oracle's bf16 flow.  The projection outputs enter the fp32 residual
+    prompts in bf16: every position of rows 0 and 1 against the fp64 oracle,
+    the oracle's bf16 flow and the reference's own bf16 flow.  The projection outputs enter the fp32 residual
     stream unrounded (with bf16-rounded deltas the oracle's flow reaches 0.029
     here, unrounded 0.0245; the GPU measured 0.026): at 48 layers bf16 operands
     for every matrix product leave ~15 % of the 3e-2 bar."""
@@ -184,11 +128,11 @@ def test_xl_bf16_prefill_all_positions(gpu):
     w32 = {k: v.float() for k, v in w.items()}
     w32["lm_head.weight"] = w32["wte"]
     del w
-    exact = R.gpt_forward(w32, ids[:2], 25, R.FLOWS["fp64"])
-    flow = R.gpt_forward(w32, ids[:2], 25, R.FLOWS["bf16"]).double()
-    e_exact = (out - exact).abs().max().item()
-    e_flow = (out - flow).abs().max().item()
-    print(f"XL b32x128 rows 0-1: max|err| vs fp64 {e_exact:.4f}, vs bf16 flow {e_flow:.4f}, "
-          f"oracle bf16 flow vs fp64 {(flow - exact).abs().max().item():.4f}; top-1 vs flow "
-          f"{agreement(out, flow) * 100:.2f}%, vs fp64 {agreement(out, exact) * 100:.2f}%")
-    assert e_exact <= 3e-2 and e_flow <= 3e-2
+    s = bf16_stats(out, w32, ids[:2], 25)
+    report("XL b32x128 rows 0-1", s)
+    assert s["err_fp64"] <= 3e-2 and s["err_flow"] <= 3e-2, s
+    assert s["err_fp64"] <= s["ref_err_fp64"], s
+    # Measured on MI355X: 98.05 % against fp64, 98.83 % against the bf16 flow.
+    assert s["top1_fp64"] >= 0.975 and s["top1_flow"] >= 0.975, s
+    assert s["top1_fp64"] >= s["ref_top1_fp64"], s
+    assert s["tie_fp64"] <= NEAR_TIE and s["tie_flow"] <= NEAR_TIE, s

@@ -166,6 +166,36 @@ def test_forward_matches_transformers_gpt2(nano):
     assert (out32.double() - ref).abs().max().item() < 1e-5
 
 
+def test_forward_matches_transformers_with_checkpoint_like_params():
+    """Every bias ~N(0, 0.1), LayerNorm gamma ~N(1, 0.1), beta ~N(0, 0.1), each
+    drawn separately: the oracle's routing of each tensor
+    (cutile_gpt/models/gpt.py:120-177) equals transformers' GPT-2 to fp64
+    rounding, and exchanging any two of them (a planted slip) moves the
+    transformers result far beyond the fp32 bar, so the comparison sees it."""
+    from tests.golden.make_golden import hf_model
+    L, H, D = 3, 3, 48
+    w = R.randomize_affine(R.init_weights(L, H, D, seed=4), seed=40)
+    for i in range(L):
+        assert not torch.equal(w[f"h.{i}.attn.c_proj.bias"], w[f"h.{i}.mlp.c_proj.bias"])
+        assert not torch.equal(w[f"h.{i}.ln_1.weight"], w[f"h.{i}.ln_2.weight"])
+        assert (w[f"h.{i}.ln_2.weight"] - 1).abs().max() > 0.1
+    assert not torch.equal(w["h.0.ln_1.bias"], w["h.1.ln_1.bias"])
+    assert w["ln_f.bias"].abs().max() > 0.1 and w["lm_head.weight"] is w["wte"]
+    ids = torch.randint(0, 50257, (2, 40), generator=torch.Generator().manual_seed(41))
+    with torch.no_grad():
+        ref = hf_model(w, L, H, D).double()(ids).logits
+    out = R.gpt_forward(w, ids, H, R.FLOWS["fp64"])
+    assert (out - ref).abs().max().item() < 1e-10
+    for a, b in (("h.0.attn.c_proj.bias", "h.0.mlp.c_proj.bias"),
+                 ("h.1.ln_1.weight", "h.1.ln_2.weight"), ("h.2.ln_1.bias", "h.2.ln_2.bias"),
+                 ("h.0.attn.c_attn.bias", "h.1.attn.c_attn.bias"),
+                 ("h.1.mlp.c_fc.bias", "h.2.mlp.c_fc.bias"), ("ln_f.bias", "h.2.ln_2.bias")):
+        bad = dict(w)
+        bad[a], bad[b] = w[b], w[a]
+        d = (R.gpt_forward(bad, ids, H, R.FLOWS["fp64"]) - ref).abs().max().item()
+        assert d > 1e-2, (a, b, d)
+
+
 def test_forward_matches_golden_fixture():
     gold = np.load(GOLDEN)
     w = R.init_weights(3, 3, 48, seed=0)

@@ -9,17 +9,17 @@ GPT-2 XL workload (batch 32; the first 8 prompts compared).
 
 Asserted per workload: every stream equals the oracle's up to its first
 differing token, and a stream may differ only at a step where the oracle's
-top-1/top-2 logit gap is within the bf16 logit tolerance (3e-2): there the two
-implementations' rounding noise decides a near-tie.  Teacher-forced on the
-oracle's streams (one forward over prompt + oracle tokens), the GPU's greedy
-choice equals the oracle's at >= 98.5 % of the 128 steps, again with every
-difference a near-tie.  The fraction of streams
-identical over all 128 steps is printed, not asserted: with random N(0, 0.02)
-weights a 128-step stream meets a near-tie (gap below ~5e-3) with high
-probability, and one flipped bf16 rounding anywhere upstream decides it, so
->= 95 % identical streams is out of reach for any two bf16 implementations
-(measured on MI355X: 8/32 at GPT-2 124M, 3/8 at XL, every divergence at a gap
-below 7e-3).
+top-1/top-2 logit gap is below NEAR_TIE (1.5e-2; the largest measured on
+MI355X is 9.8e-3, at XL depth): there the two implementations' rounding noise decides
+a near-tie.  Teacher-forced on the oracle's streams (one forward over prompt +
+oracle tokens), the GPU's greedy choice equals the oracle's at no fewer steps
+than a floor just under the measured agreement, again with every difference a
+near-tie.  The fraction of streams identical over all 128 steps has a floor
+under its measured value too (8/32 at GPT-2 124M, 3/8 at XL), so that a
+precision regression fails; >= 95 % identical streams is out of reach for any
+two bf16 implementations with random N(0, 0.02) weights: a 128-step stream
+meets a near-tie (gap below ~5e-3) with high probability, and one flipped bf16
+rounding anywhere upstream decides it.
 
 Reference: ``cutile_gpt/models/gpt.py:185-229`` (generate with top_k=1).
 """
@@ -35,7 +35,10 @@ from tests.golden.make_streams import CONFIGS, NEW, weights
 
 pytestmark = pytest.mark.gpu
 HERE = os.path.join(os.path.dirname(__file__), "golden")
-NEAR_TIE = 3e-2
+NEAR_TIE = 1.5e-2
+# Floors under the MI355X measurements (GPT-2: 8/32 streams, 98.90 % of steps;
+# XL: 3/8, 99.32 %): (identical streams, teacher-forced steps).
+FLOORS = {"gpt2": (6 / 32, 0.987), "xl": (2 / 8, 0.990)}
 
 
 def compare_streams(name, gpu, use_graph=True):
@@ -76,5 +79,7 @@ def test_bf16_greedy_streams_vs_oracle(gpu, name):
     frac, report, step_agree, forced_gaps = compare_streams(name, gpu)
     for r, step, g in report:
         assert g <= NEAR_TIE, f"row {r} diverged at step {step} where the oracle's gap is {g:.3e}"
-    assert step_agree >= 0.985
-    assert (forced_gaps <= NEAR_TIE).all()
+    same_floor, step_floor = FLOORS[name]
+    assert frac >= same_floor, frac
+    assert step_agree >= step_floor, step_agree
+    assert (forced_gaps <= NEAR_TIE).all(), forced_gaps.max()
