@@ -1945,11 +1945,10 @@ extern "C" int cgpt_gemm(const void* a, const void* w, const void* bias, void* c
   const int64_t out_align = out16 ? 8 : 16;
   const bool vec_store = (ldc % 4 == 0) && (reinterpret_cast<uintptr_t>(c) % out_align == 0);
   if (tile == CGPT_TILE_SKINNY && (el || f16)) return CGPT_EINVAL;  // vector-rule bf16 / fp32 only
-  if (tile != CGPT_TILE_AUTO && tile != CGPT_TILE_SKINNY && (tile < 0 || tile >= nt))
-    return CGPT_EINVAL;
   if (epilogue == CGPT_EPI_BIAS_RESID) {
     if (tile == CGPT_TILE_SKINNY) return CGPT_EINVAL;  // not a skinny epilogue
-    // launch_resid picks the kernel (tile: a preference).
+    // launch_resid picks the kernel (tile: a preference; an id it does not
+    // take for these dtypes, in or out of the tile tables, means TILE_AUTO).
     if (el) {
       if (f16)
         return out16 ? launch_epi<f16_t, f16_t>(epilogue, 0, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, true, s)
@@ -1971,6 +1970,8 @@ extern "C" int cgpt_gemm(const void* a, const void* w, const void* bias, void* c
       return launch_resid<float, float>(tile, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, s);
     return launch_resid<float, bf16_t>(tile, a, w, bias, bb, c, m, n, k, lda, ldw, ldc, vec_store, s);
   }
+  if (tile != CGPT_TILE_AUTO && tile != CGPT_TILE_SKINNY && (tile < 0 || tile >= nt))
+    return CGPT_EINVAL;
   if (tile == CGPT_TILE_AUTO && M <= 64 && !el && !f16) tile = CGPT_TILE_SKINNY;
   if (tile == CGPT_TILE_SKINNY) {
     if (M > 64) return CGPT_ESHAPE;

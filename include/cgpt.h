@@ -10,8 +10,13 @@
  *       0            CGPT_OK
  *       < 0          an argument error (CGPT_E*), nothing was launched
  *       > 0          a hipError_t from the launch
- *   - has no mutable global state, so concurrent calls on different streams
- *     are safe.
+ *   - keeps no state between calls except (a) per-device caches of the CU
+ *     count and of kernel occupancies, filled on first use through atomics
+ *     and read-only afterwards, safe from any thread, and (b) the per-GPU
+ *     scratch array of cgpt_gemm_skinny_noalloc, which overlapping calls of
+ *     that entry point on one GPU share and race on.  Every other entry point
+ *     works only in the caller's buffers: concurrent calls on different
+ *     streams are safe when their outputs (and workspaces) are distinct.
  *
  * Element types are CGPT_F32 (IEEE fp32), CGPT_BF16 (bfloat16 bit patterns)
  * and CGPT_F16 (IEEE binary16; the GEMM, LayerNorm, GELU, attention and

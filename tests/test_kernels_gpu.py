@@ -540,6 +540,53 @@ def test_gemm_residual_epilogue_slab(gpu, m, n, k):
     assert err <= 2e-4 * math.sqrt(k / 64), err
 
 
+@pytest.mark.parametrize("tile", [14, _lib.TILE_AUTO])
+@pytest.mark.parametrize("m,n,k", [(32768, 768, 768), (16384, 1536, 768), (8192, 2304, 512)])
+def test_gemm_residual_epilogue_slab_multi_tile(gpu, tile, m, n, k):
+    """The slab kernel's residual ring when a persistent block walks two tiles
+    (512 / 512 / 384 tiles of 256x192 for 256 CUs): the first two C row blocks
+    of a block's next tile are fetched into its LDS ring during the current
+    tile's last two K steps, with the current tile's stores still in flight;
+    K = 512 gives exactly 8 k64 steps, one per ring row.  TILE_AUTO takes the
+    slab kernel here too (at least one tile per CU).  Against the fp64 sum."""
+    g = torch.Generator(device=gpu).manual_seed(m + 5 * n + k + tile)
+    a = torch.randn(m, k, device=gpu, generator=g).to(BF16)
+    w = (torch.randn(n, k, device=gpu, generator=g) * 0.05).to(BF16)
+    b = torch.randn(n, device=gpu, generator=g).to(BF16)
+    x = torch.randn(m, n, device=gpu, generator=g) * 4
+    ref = x.double() + a.double() @ w.double().t() + b.double()
+    c = x.clone()
+    _resid_gemm(a, w, b, c, tile=tile)
+    err = (c.double() - ref).abs().max().item()
+    assert err <= 2e-4 * math.sqrt(k / 64), err
+
+
+@pytest.mark.parametrize("dt,tiles", [(F32, [14, 17, 19, 5, 2, -5, 99]),
+                                      (BF16, [5, 16, -7, 99])])
+def test_gemm_residual_unknown_tile_ids_mean_auto(gpu, dt, tiles):
+    """With the residual epilogue a tile id the dtype does not take (fp32 with a
+    bf16-only id, a persistent non-residual id, a negative id other than AUTO /
+    SKINNY, an id past the tables) runs as TILE_AUTO: status OK and the
+    TILE_AUTO result bit for bit."""
+    m, n, k = 520, 264, 512
+    a = randn(m, k, seed=61, dtype=dt).to(gpu)
+    w = randn(n, k, seed=62, dtype=dt, scale=0.05).to(gpu)
+    b = randn(n, seed=63, dtype=dt).to(gpu)
+    x = randn(m, n, seed=64, scale=3.0).to(gpu)
+    ref = x.clone()
+    _resid_gemm(a, w, b, ref, tile=_lib.TILE_AUTO)
+    for t in tiles:
+        c = x.clone()
+        _resid_gemm(a, w, b, c, tile=t)
+        assert torch.equal(c, ref), t
+    # Without the residual epilogue such ids are still rejected.
+    lib = _lib.load()
+    code = {F32: _lib.CGPT_F32, BF16: _lib.CGPT_BF16}[dt]
+    out = torch.empty(m, n, device=gpu)
+    assert lib.cgpt_gemm(a.data_ptr(), w.data_ptr(), b.data_ptr(), out.data_ptr(), m, n, k, k, k,
+                         n, code, code, _lib.CGPT_F32, _lib.EPI_BIAS, 99, None) == -1
+
+
 @pytest.mark.parametrize("tile", [_lib.TILE_AUTO, 0, 1, 2, 3, 4, 9])
 @pytest.mark.parametrize("m,n,k", [(4096, 512, 2048), (300, 520, 512), (513, 200, 640)])
 def test_gemm_residual_epilogue_tiles(gpu, tile, m, n, k):
