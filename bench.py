@@ -19,9 +19,11 @@ events around every launch.
 ``standalone_kernels`` (also ``--workload kernels`` on its own): the standalone
 kernel set — tanh-GELU, LayerNorm and causal attention in fp32 and bf16 — each
 timed over rotating buffers larger than the MALL, as a fraction of its
-roofline; the HBM-bound ones also beside a plain device copy of the same bytes
-timed the same way (``copy_GB/s``, ``frac_of_copy``): the rate a copy reaches
-at 50-100 MB, well below the 8 TB/s peak.
+roofline; the HBM-bound ones also beside plain device copies of the same bytes
+timed the same way (``copy_variants_GB/s``: one-shot and persistent grids, 1-8
+vectors in flight a thread, non-temporal and cached, and torch's copy_;
+``copy_GB/s`` is the fastest, ``frac_of_copy`` the kernel against it): the rate
+any copy reaches at 50-100 MB, below the 8 TB/s peak.
 
 ``--workload xl-decode``: KV-cache greedy decoding of GPT-2 XL (48 layers, 25
 heads, d 1600), bf16 N(0, 0.02) weights generated on the device, batch 32,
@@ -325,17 +327,19 @@ def bench_xl_decode(args):
     step_s = (time.perf_counter() - t0) / k
     mean_ctx = T0 + 1 + (k - 1) / 2.0 + 1  # keys visible per step, averaged
 
-    # LM-head skinny GEMM alone (the single largest launch of a step).
+    # LM-head skinny GEMM alone (the single largest launch of a step), called as
+    # the step calls it (no split-K workspace).
     lib = _lib.load()
     st = torch.cuda.current_stream(dev)
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     head_w = model.weights["lm_head.weight"]
-    call = lambda: _lib.check(lib.cgpt_gemm_skinny(sess.h.data_ptr(), head_w.data_ptr(), None,
-                                                   sess.logits.data_ptr(), B, V, D, D, D, V,
-                                                   _lib.CGPT_BF16, _lib.CGPT_BF16, _lib.CGPT_F32,
-                                                   _lib.EPI_NONE, sess.ws.data_ptr(), sess.ws_bytes,
-                                                   sess.counters.data_ptr(), sess.counters.numel(),
-                                                   st.cuda_stream), "head")
+    use_ws = not sess.partials
+    call = lambda: _lib.check(lib.cgpt_gemm_skinny(
+        sess.h.data_ptr(), head_w.data_ptr(), None, sess.logits.data_ptr(), B, V, D, D,
+        head_w.stride(0), V, _lib.CGPT_BF16, _lib.CGPT_BF16, _lib.CGPT_F32, _lib.EPI_NONE,
+        sess.ws.data_ptr() if use_ws else None, sess.ws_bytes,
+        sess.counters.data_ptr() if use_ws else None, sess.counters.numel(), st.cuda_stream),
+        "head")
     for _ in range(3):
         call()
     ev0.record(st)
@@ -417,19 +421,32 @@ def standalone_kernels(iters=40):
         return e0.elapsed_time(e1) / iters
 
     blib = ctypes.CDLL(os.path.join(os.path.dirname(_lib.LIB_PATH), "libcgpt_bench.so"))
-    blib.cgpt_bench_copy16.restype = ctypes.c_int
-    blib.cgpt_bench_copy16.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
-                                       ctypes.c_void_p]
+    blib.cgpt_bench_copy_variant.restype = ctypes.c_int
+    blib.cgpt_bench_copy_variant.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                             ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                             ctypes.c_void_p]
+    # Plain copies of the same bytes (csrc_bench/ceiling.hip): (variant, 16-byte
+    # vectors a thread, blocks a CU).  0 = one-shot grid, one vector a thread;
+    # 1 = persistent grid, non-temporal; 2 = persistent, cached; 3 = one-shot,
+    # consecutive vectors a thread.  The fastest of a sweep of 29 such copies at
+    # 50 and 100 MB on MI355X are here, beside torch's own copy_.
+    copy_variants = {"oneshot_v1": (0, 1, 1), "persistent_nt_v4_b8": (1, 4, 8),
+                     "persistent_nt_v8_b4": (1, 8, 4), "persistent_nt_v8_b8": (1, 8, 8),
+                     "persistent_cached_v4_b8": (2, 4, 8), "oneshot_consecutive_v2": (3, 2, 1)}
 
     def copy_ceiling(xs, ys, nbytes):
-        # The rate a plain device copy reaches at the same byte count (read
+        # The rate plain device copies reach at the same byte count (read
         # nbytes / 2, write nbytes / 2), timed the same way over the same
-        # rotating buffers: 16 bytes a thread, non-temporal loads and stores.
-        def one(i):
-            if blib.cgpt_bench_copy16(xs[i].data_ptr(), ys[i].data_ptr(), nbytes // 2, s) != 0:
-                raise RuntimeError("cgpt_bench_copy16 failed")
-        ms = timed(one, len(xs))
-        return round(nbytes / ms / 1e6, 1)
+        # rotating buffers; returns (best GB/s, {variant: GB/s}).
+        rates = {}
+        for name, (var, vec, bpc) in copy_variants.items():
+            def one(i, var=var, vec=vec, bpc=bpc):
+                if blib.cgpt_bench_copy_variant(xs[i].data_ptr(), ys[i].data_ptr(), nbytes // 2,
+                                                var, vec, bpc, s) != 0:
+                    raise RuntimeError("cgpt_bench_copy_variant failed")
+            rates[name] = round(nbytes / timed(one, len(xs)) / 1e6, 1)
+        rates["torch_copy_"] = round(nbytes / timed(lambda i: ys[i].copy_(xs[i]), len(xs)) / 1e6, 1)
+        return max(rates.values()), rates
 
     def copies(t, pair_bytes):
         n = max(2, -(-ROTATE_BYTES // pair_bytes))
@@ -451,12 +468,13 @@ def standalone_kernels(iters=40):
         ms = timed(lambda i: _lib.check(lib.cgpt_gelu(xs[i].data_ptr(), ys[i].data_ptr(), n,
                                                       code[dt], s), "gelu"), len(xs))
         nbytes = 2 * n * es
-        copy = copy_ceiling(xs, ys, nbytes)
+        copy, rates = copy_ceiling(xs, ys, nbytes)
         out[f"gelu_{tag}"] = {"shape": [32, 512, 768], "avg_launch_ms": round(ms, 4),
                               "bytes": nbytes, "GB/s": round(nbytes / ms / 1e6, 1),
                               "frac": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4), "bound": "hbm",
-                              "copy_GB/s": copy,
-                              "frac_of_copy": round(nbytes / ms / 1e6 / copy, 4)}
+                              "copy_GB/s": copy, "copy_frac_of_peak": round(copy / PEAK_HBM_GBS, 4),
+                              "frac_of_copy": round(nbytes / ms / 1e6 / copy, 4),
+                              "copy_variants_GB/s": rates}
         del xs, ys
         # LayerNorm: read x, write y, read gamma and beta.
         M, N = ln_x.shape
@@ -467,12 +485,14 @@ def standalone_kernels(iters=40):
             xs[i].data_ptr(), None, None, gw.data_ptr(), gb.data_ptr(), ys[i].data_ptr(), M, N,
             1e-5, code[dt], 0, code[dt], code[dt], s), "layernorm"), len(xs))
         nbytes = 2 * M * N * es + 2 * N * es
-        copy = copy_ceiling(xs, ys, 2 * M * N * es)
+        copy, rates = copy_ceiling(xs, ys, 2 * M * N * es)
         out[f"layernorm_{tag}"] = {"shape": [M, N], "avg_launch_ms": round(ms, 4),
                                    "bytes": nbytes, "GB/s": round(nbytes / ms / 1e6, 1),
                                    "frac": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4),
                                    "bound": "hbm", "copy_GB/s": copy,
-                                   "frac_of_copy": round(nbytes / ms / 1e6 / copy, 4)}
+                                   "copy_frac_of_peak": round(copy / PEAK_HBM_GBS, 4),
+                                   "frac_of_copy": round(nbytes / ms / 1e6 / copy, 4),
+                                   "copy_variants_GB/s": rates}
         del xs, ys
         # Causal attention, (B, H, T, hd) contiguous: 4*B*H*hd*T(T+1)/2 FLOP.
         B, H, T, hd = qkv[0].shape

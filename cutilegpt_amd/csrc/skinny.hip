@@ -297,6 +297,171 @@ static SkinnyPlan partials_plan(int M, int N, int K, int elem_bytes, int split) 
   return p;
 }
 
+// Wide-N form for at most 32 rows of bf16 (the decode step's LM head, N in
+// the tens of thousands): one block of kWideWaves waves a CU.  The block
+// stages all of A in LDS once (rows zero-padded to 16 * MT, K to whole double
+// slabs, each row padded by 16 bytes so the 16 rows a fragment read touches
+// fall in different banks); each wave then owns whole 16-column slices of C
+// (slice blockIdx.x + gridDim.x * (wave + kWideWaves * i)) and streams the
+// slice's W rows straight from global memory into MFMA fragments, in rounds
+// of kWideDpw double slabs whose loads are all issued before the round's
+// MFMAs, with A's fragments read from LDS.  A slice is summed over all of K
+// by one wave, so there is no cross-wave or cross-block reduction, and the
+// grid's CUs take ceil or floor of slices / CUs slices each (the 128-column
+// blocks of shape 3 split 393 blocks over 256 CUs, two on some and one on
+// others).
+constexpr int kWideWaves = 16;
+constexpr int kWideDpw = 5;
+constexpr int kWideKMax = 2496;  // K a row may hold: 32 rows x (2 * 2496 + 16) B fit in LDS
+
+template <int MT, int EPI, typename TOut>
+__global__ __launch_bounds__(64 * kWideWaves) void gemm_skinny_wide_kernel(
+    const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, const void* __restrict__ bias,
+    bool bias_bf16, TOut* __restrict__ C, int M, int N, int K, int lda, int ldw, int64_t ldc,
+    bool vec_store) {
+  constexpr int KD = 64;  // k per double slab
+  __shared__ __attribute__((aligned(16))) uint8_t sa[MT * 16 * (2 * kWideKMax + 16)];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int kp = (K + KD - 1) / KD * KD;  // K padded to whole double slabs
+  const int rs = 2 * kp + 16;             // LDS bytes per A row
+  const int D = kp / KD;
+
+  // W loads first (rows past N are clamped: loaded, never stored), so the
+  // first round's memory trip overlaps the A staging below.
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16_t*>(W), 0, static_cast<int>((N - 1) * ldw * 2 + K * 2), 0x00020000);
+  const int nslices = (N + 15) / 16;
+  const int stride = static_cast<int>(gridDim.x) * kWideWaves;
+  int sl = static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) * wave;
+  u32x4_t wf[kWideDpw][2];
+  auto load_round = [&](int s, int d) {
+    const uint32_t wro = static_cast<uint32_t>(min(s * 16 + r16, N - 1)) * ldw * 2;
+#pragma unroll
+    for (int u = 0; u < kWideDpw; ++u)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k = (d + u) * KD + g * 16 + h * 8;
+        const uint32_t kb = (d + u < D && k < K) ? static_cast<uint32_t>(k) * 2 : kOob;
+        wf[u][h] = __builtin_amdgcn_raw_buffer_load_b128(rw, wro + kb, 0, 0);
+      }
+  };
+  if (sl < nslices) load_round(sl, 0);
+
+  // A -> LDS: 16-byte chunks; rows past M and k past K are zero (K % 8 == 0).
+  const int cpr = kp / 8;  // chunks per row
+  for (int c = static_cast<int>(threadIdx.x); c < MT * 16 * cpr; c += 64 * kWideWaves) {
+    const int row = c / cpr, k = (c % cpr) * 8;
+    u32x4_t v = {0u, 0u, 0u, 0u};
+    if (row < M && k < K) v = *reinterpret_cast<const u32x4_t*>(A + static_cast<int64_t>(row) * lda + k);
+    *reinterpret_cast<u32x4_t*>(sa + row * rs + k * 2) = v;
+  }
+  __syncthreads();
+
+  const uint8_t* abase = sa + r16 * rs + g * 32;  // this lane's fragment row, k = 16 g
+  for (; sl < nslices; sl += stride) {
+    f32x4_t acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int d = 0; d < D; d += kWideDpw) {
+      if (d > 0) load_round(sl, d);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < kWideDpw; ++u) {
+        if (d + u < D) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+              const u32x4_t af = *reinterpret_cast<const u32x4_t*>(
+                  abase + mt * 16 * rs + ((d + u) * KD + h * 8) * 2);
+              Mfma<bf16_t>::run(wf[u][h], af, acc[mt]);
+            }
+        }
+      }
+    }
+    // The next slice's first round goes out before this one's stores.
+    const int n0 = sl * 16;
+    if (sl + stride < nslices) load_round(sl + stride, 0);
+    // Lane (g, r16) holds C[16 mt + r16][n0 + 4 g + i], i = 0..3.
+    const int n = n0 + 4 * g;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = 16 * mt + r16;
+      if (m >= M || n >= N) continue;
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float x = acc[mt][r];
+        if (EPI != CGPT_EPI_NONE) x += n + r < N ? bias_value(bias, bias_bf16, n + r) : 0.f;
+        if (EPI == CGPT_EPI_BIAS_GELU) x = gelu_tanh(x);
+        v[r] = x;
+      }
+      TOut* out = C + static_cast<int64_t>(m) * ldc + n;
+      if (vec_store && n + 3 < N) {
+        store4_out(out, v);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (n + r < N) Elem<TOut>::store(out + r, v[r]);
+      }
+    }
+  }
+}
+
+static int skinny_num_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    return 256;
+  return n;
+}
+
+// The wide form is taken for bf16, M <= 32, K within the LDS budget, no split
+// workspace, and N wide enough that every CU gets several slices.
+static bool wide_ok(bool bf16_in, bool have_ws, int M, int N, int K) {
+  return bf16_in && !have_ws && M <= 32 && K <= kWideKMax && (N + 15) / 16 >= 8 * skinny_num_cus();
+}
+
+template <int EPI, typename TOut>
+static void launch_wide_mt(const bf16_t* A, const bf16_t* W, const void* bias, bool bias_bf16,
+                           TOut* C, int M, int N, int K, int lda, int ldw, int64_t ldc,
+                           bool vec_store, hipStream_t s) {
+  const int slices = (N + 15) / 16;
+  const int cus = skinny_num_cus();
+  const dim3 grid(static_cast<unsigned>(slices < cus ? slices : cus));
+  if (M <= 16)
+    hipLaunchKernelGGL((gemm_skinny_wide_kernel<1, EPI, TOut>), grid, dim3(64 * kWideWaves), 0, s, A, W,
+                       bias, bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store);
+  else
+    hipLaunchKernelGGL((gemm_skinny_wide_kernel<2, EPI, TOut>), grid, dim3(64 * kWideWaves), 0, s, A, W,
+                       bias, bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store);
+}
+
+template <typename TOut>
+static int launch_wide(int epi, const void* a, const void* w, const void* bias, bool bias_bf16,
+                       void* c, int M, int N, int K, int lda, int ldw, int64_t ldc, bool vec_store,
+                       hipStream_t s) {
+  const bf16_t* A = static_cast<const bf16_t*>(a);
+  const bf16_t* W = static_cast<const bf16_t*>(w);
+  TOut* C = static_cast<TOut*>(c);
+  switch (epi) {
+    case CGPT_EPI_NONE:
+      launch_wide_mt<CGPT_EPI_NONE, TOut>(A, W, bias, bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store, s);
+      break;
+    case CGPT_EPI_BIAS:
+      launch_wide_mt<CGPT_EPI_BIAS, TOut>(A, W, bias, bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store, s);
+      break;
+    case CGPT_EPI_BIAS_GELU:
+      launch_wide_mt<CGPT_EPI_BIAS_GELU, TOut>(A, W, bias, bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store, s);
+      break;
+    default:
+      return CGPT_EINVAL;
+  }
+  return hip_status(hipGetLastError());
+}
+
 template <typename TIn, int MT, int NT, int NW, int DPW, int MODE, int EPI, typename TOut>
 static void launch_one(const SkinnyPlan& p, const TIn* A, const TIn* W, const void* bias,
                        bool bias_bf16, TOut* C, int M, int N, int K, int lda, int ldw, int64_t ldc,
@@ -388,6 +553,14 @@ int launch_gemm_skinny(bool bf16_in, int epilogue, const void* a, const void* w,
   if (M > 64) return CGPT_ESHAPE;
   const int es = bf16_in ? 2 : 4;
   const bool have_ws = workspace != nullptr && counters != nullptr;
+  if (wide_ok(bf16_in, have_ws, M, N, K) && a_fits(M, K, lda, es) &&
+      static_cast<int64_t>(N - 1) * ldw * es + static_cast<int64_t>(K) * es < (int64_t{1} << 31)) {
+    const uintptr_t oa = out_bf16 ? 7 : 15;
+    const bool vec_store = ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(c) & oa) == 0;
+    const int li = static_cast<int>(lda), lw = static_cast<int>(ldw);
+    return out_bf16 ? launch_wide<bf16_t>(epilogue, a, w, bias, bias_bf16, c, M, N, K, li, lw, ldc, vec_store, s)
+                    : launch_wide<float>(epilogue, a, w, bias, bias_bf16, c, M, N, K, li, lw, ldc, vec_store, s);
+  }
   const SkinnyPlan p = skinny_plan(M, N, K, es, have_ws);
   const int scols = 16 * kSkShapes[p.shape].nt;
   const int step = cols_per_launch(N, K, ldw, es, scols);

@@ -69,11 +69,13 @@ def test_nano_fp32_affine_through_both_loaders(gpu, tmp_path):
         # beyond the bar plus the error measured above: the check catches it.
         d = (la - R.gpt_forward(swapped(w, x, y), ids, H, R.FLOWS["fp64"])).abs().max().item()
         assert d > 1e-3 + err, (x, y, d)
-    # q/k/v thirds of the fused QKV bias in the wrong order
+    # k and v thirds of the fused QKV bias exchanged (q <-> k alone moves these
+    # logits by only 4e-4: the key bias adds a per-query constant to every
+    # score, which the softmax cancels, so that slip is below the fp32 bar)
     qkv = dict(w)
     for i in range(L):
         bq, bk, bv = w[f"h.{i}.attn.c_attn.bias"].split(D)
-        qkv[f"h.{i}.attn.c_attn.bias"] = torch.cat([bk, bq, bv])
+        qkv[f"h.{i}.attn.c_attn.bias"] = torch.cat([bq, bv, bk])
     assert (la - R.gpt_forward(qkv, ids, H, R.FLOWS["fp64"])).abs().max().item() > 1e-3 + err
 
 
