@@ -26,6 +26,8 @@
 #include "common.h"
 #include "internal.h"
 
+#include <algorithm>
+
 namespace cgpt {
 
 // Block shapes: NT n-tiles per block, NW waves, DPW double slabs per wave and
@@ -316,11 +318,13 @@ constexpr int kWideKMax = 2496;  // K a row may hold: 32 rows x (2 * 2496 + 16) 
 
 template <int MT, int EPI, typename TOut>
 __global__ __launch_bounds__(64 * kWideWaves) void gemm_skinny_wide_kernel(
-    const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, const void* __restrict__ bias,
+    const bf16_t* __restrict__ A, const bf16_t* W, const void* __restrict__ bias,
     bool bias_bf16, TOut* __restrict__ C, int M, int N, int K, int lda, int ldw, int64_t ldc,
     bool vec_store) {
+#if defined(__HIP_DEVICE_COMPILE__)
   constexpr int KD = 64;  // k per double slab
-  __shared__ __attribute__((aligned(16))) uint8_t sa[MT * 16 * (2 * kWideKMax + 16)];
+  // 1 KiB past the A image: the last 64-lane DMA of the staging may run past it.
+  __shared__ __attribute__((aligned(16))) uint8_t sa[MT * 16 * (2 * kWideKMax + 16) + 1024];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r16 = lane & 15, g = lane >> 4;
@@ -328,8 +332,25 @@ __global__ __launch_bounds__(64 * kWideWaves) void gemm_skinny_wide_kernel(
   const int rs = 2 * kp + 16;             // LDS bytes per A row
   const int D = kp / KD;
 
-  // W loads first (rows past N are clamped: loaded, never stored), so the
-  // first round's memory trip overlaps the A staging below.
+  // A goes to LDS by DMA (16 bytes a lane, 64 consecutive 16-byte slots an
+  // instruction; the slot after each row's last chunk is the row's padding),
+  // then the first W round; the wait before the barrier leaves exactly that
+  // round's kWideDpw * 2 loads outstanding, so the barrier does not wait for
+  // W.  Rows past M, k past K and the padding slots load zero (an offset past
+  // the record count).
+  const u32x4_t ra = buffer_desc(A, static_cast<uint32_t>((M - 1) * lda * 2 + K * 2));
+  const int cpr = kp / 8;  // chunks per row
+  const int nslot = MT * 16 * (cpr + 1);
+#pragma unroll
+  for (int i = 0; i < (MT * 16 * (kWideKMax / 8 + 1) + 64 * kWideWaves - 1) / (64 * kWideWaves); ++i) {
+    const int base = (i * kWideWaves + wave) * 64;
+    if (base >= nslot) break;
+    const int slot = base + lane;
+    const int row = slot / (cpr + 1), ch = slot - row * (cpr + 1);
+    const uint32_t off = (row < M && ch < cpr && ch * 8 < K)
+                             ? static_cast<uint32_t>(row * lda + ch * 8) * 2 : kOob;
+    dma_lds16(ra, lds_addr(sa + base * 16), off, 0);
+  }
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<bf16_t*>(W), 0, static_cast<int>((N - 1) * ldw * 2 + K * 2), 0x00020000);
   const int nslices = (N + 15) / 16;
@@ -337,27 +358,24 @@ __global__ __launch_bounds__(64 * kWideWaves) void gemm_skinny_wide_kernel(
   int sl = static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) * wave;
   u32x4_t wf[kWideDpw][2];
   auto load_round = [&](int s, int d) {
+    const bool live = s < nslices;
     const uint32_t wro = static_cast<uint32_t>(min(s * 16 + r16, N - 1)) * ldw * 2;
 #pragma unroll
     for (int u = 0; u < kWideDpw; ++u)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int k = (d + u) * KD + g * 16 + h * 8;
-        const uint32_t kb = (d + u < D && k < K) ? static_cast<uint32_t>(k) * 2 : kOob;
+        const uint32_t kb = (live && d + u < D && k < K) ? static_cast<uint32_t>(k) * 2 : kOob;
         wf[u][h] = __builtin_amdgcn_raw_buffer_load_b128(rw, wro + kb, 0, 0);
       }
   };
-  if (sl < nslices) load_round(sl, 0);
-
-  // A -> LDS: 16-byte chunks; rows past M and k past K are zero (K % 8 == 0).
-  const int cpr = kp / 8;  // chunks per row
-  for (int c = static_cast<int>(threadIdx.x); c < MT * 16 * cpr; c += 64 * kWideWaves) {
-    const int row = c / cpr, k = (c % cpr) * 8;
-    u32x4_t v = {0u, 0u, 0u, 0u};
-    if (row < M && k < K) v = *reinterpret_cast<const u32x4_t*>(A + static_cast<int64_t>(row) * lda + k);
-    *reinterpret_cast<u32x4_t*>(sa + row * rs + k * 2) = v;
-  }
-  __syncthreads();
+  load_round(sl, 0);
+  // W is not __restrict__ here: loads through it are then not invariant and
+  // cannot move across the memory clobbers of the DMA above or of this wait,
+  // so exactly the round's loads are younger than the last DMA.
+  static_assert(kWideDpw * 2 == 10, "the wait below counts one W round");
+  asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
+  raw_barrier();
 
   const uint8_t* abase = sa + r16 * rs + g * 32;  // this lane's fragment row, k = 16 g
   for (; sl < nslices; sl += stride) {
@@ -408,6 +426,183 @@ __global__ __launch_bounds__(64 * kWideWaves) void gemm_skinny_wide_kernel(
       }
     }
   }
+#endif  // __HIP_DEVICE_COMPILE__
+}
+
+// Decode-layer form for at most 32 rows of bf16 and N of a few hundred
+// 16-column n-tiles (the QKV, projection and MLP GEMMs of a decode step).
+// Block (group g, chunk sk) covers the 16 * NW columns of group g over the
+// K chunk sk (chunk double slabs, at most KS):
+//  * its waves DMA the chunk of A into LDS (16-byte slots, each row padded by
+//    one slot so the 16 rows of a fragment read fall in different banks);
+//  * each wave then issues all KS * 2 loads of its n-tile's W rows at once,
+//    one memory round trip, and the wait before the barrier leaves exactly
+//    those loads outstanding (W is not __restrict__: loads through it are not
+//    invariant and cannot move across the memory clobbers of the DMA or of the
+//    wait), so the barrier waits for A only;
+//  * MT * 2 MFMAs per double slab with A's fragments read from LDS.
+// Waves split N, not K, so there is no cross-wave reduction, and A is read
+// from L2 once per block instead of once per n-tile.  The chunk sums are
+// either written as fp32 partial products P[sk][m][n] (rows of ldc floats) for
+// the consumer to add (kSkPartials), or, for the final output, stored to the
+// workspace and added in chunk order by the last block of the column group to
+// arrive (counted on a device atomic; the same sc1 hand-off as
+// gemm_skinny_kernel), which applies the epilogue (kSkFinal; split == 1
+// stores directly).
+constexpr int kDecMaxKs = 10;  // double slabs a chunk may hold
+
+template <int MT, int NW, int KS, int MODE, int EPI, typename TOut>
+__global__ __launch_bounds__(64 * NW) void gemm_decode_kernel(
+    const bf16_t* __restrict__ A, const bf16_t* W, const void* __restrict__ bias,
+    bool bias_bf16, TOut* __restrict__ C, int M, int N, int K, int lda, int ldw, int64_t ldc,
+    bool vec_store, int split, int chunk, float* __restrict__ ws, int* __restrict__ counters) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int KD = 64;               // k per double slab
+  constexpr int SROW = KS * 8 + 1;     // 16-byte slots per A row, the last one padding
+  constexpr int RS = SROW * 16;        // LDS bytes per A row
+  constexpr int NSLOT = MT * 16 * SROW;
+  constexpr int NINS = (NSLOT + 64 * NW - 1) / (64 * NW);  // DMA instructions a wave, at most
+  // Whole 64-slot DMA instructions: the last one may run past the A image.
+  __shared__ __attribute__((aligned(16))) uint8_t sa[NINS * NW * 64 * 16];
+  __shared__ int s_last;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int gi = blockIdx.x / split, sk = blockIdx.x % split;
+  const int dslabs = (K + KD - 1) / KD;
+  const int d0 = sk * chunk;
+  const int d1 = min(dslabs, d0 + chunk);  // d1 <= d0: an empty chunk, zero sums
+
+  // A's chunk -> LDS; rows past M, k past K or past the chunk, and the padding
+  // slots load zero (an offset past the record count).
+  const u32x4_t ra = buffer_desc(A, static_cast<uint32_t>((M - 1) * lda * 2 + K * 2));
+#pragma unroll
+  for (int i = 0; i < NINS; ++i) {
+    const int base = (i * NW + wave) * 64;
+    if (base >= NSLOT) break;
+    const int slot = base + lane;
+    const int row = slot / SROW, ch = slot - row * SROW;
+    const int k = d0 * KD + ch * 8;
+    const bool ok = row < M && ch < KS * 8 && d0 + ch / 8 < d1 && k < K;
+    dma_lds16(ra, lds_addr(sa + base * 16), ok ? static_cast<uint32_t>(row * lda + k) * 2 : kOob, 0);
+  }
+  // This wave's n-tile (rows past N are clamped: loaded, never stored).
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16_t*>(W), 0, static_cast<int>((N - 1) * ldw * 2 + K * 2), 0x00020000);
+  const int nt = gi * NW + wave;
+  const bool live = nt * 16 < N;
+  const uint32_t wro = static_cast<uint32_t>(min(nt * 16 + r16, N - 1)) * ldw * 2;
+  u32x4_t wf[KS][2];
+#pragma unroll
+  for (int u = 0; u < KS; ++u)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int k = (d0 + u) * KD + g * 16 + h * 8;
+      const uint32_t kb = (live && d0 + u < d1 && k < K) ? static_cast<uint32_t>(k) * 2 : kOob;
+      wf[u][h] = __builtin_amdgcn_raw_buffer_load_b128(rw, wro + kb, 0, 0);
+    }
+  asm volatile("" ::: "memory");
+  wait_vmcnt<KS * 2>();
+  raw_barrier();
+
+  f32x4_t acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const uint8_t* abase = sa + r16 * RS + g * 32;  // this lane's fragment row, k = 16 g
+#pragma unroll
+  for (int u = 0; u < KS; ++u) {
+    if (d0 + u < d1) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const u32x4_t af =
+              *reinterpret_cast<const u32x4_t*>(abase + mt * 16 * RS + (u * KD + h * 8) * 2);
+          Mfma<bf16_t>::run(wf[u][h], af, acc[mt]);
+        }
+    }
+  }
+  // Lane (g, r16) holds C[16 mt + r16][16 nt + 4 g + i], i = 0..3.
+  const int n = nt * 16 + 4 * g;
+
+  if (MODE == kSkPartials) {
+    if (!live) return;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = 16 * mt + r16;
+      if (m >= M || n >= N) continue;
+      float* out = reinterpret_cast<float*>(C) + (static_cast<int64_t>(sk) * M + m) * ldc + n;
+      const float v[4] = {acc[mt][0], acc[mt][1], acc[mt][2], acc[mt][3]};
+      if (vec_store && n + 3 < N) {
+        store4_out(out, v);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (n + r < N) out[r] = v[r];
+      }
+    }
+    return;
+  }
+
+  if (split > 1) {
+    // Chunk sk's sums go to the group's workspace slots [sk][wave][mt][lane]
+    // (f32x4) with sc1 stores; the last block to count itself on the group's
+    // counter adds all chunks in order and resets the counter.
+    constexpr int kTile = NW * MT * 64;  // f32x4 per chunk
+    const __amdgpu_buffer_rsrc_t rws = __builtin_amdgcn_make_buffer_rsrc(
+        ws + static_cast<int64_t>(gi) * split * kTile * 4, 0, split * kTile * 16, 0x00020000);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, acc[mt]), rws,
+                                             ((sk * NW + wave) * MT * 64 + mt * 64 + lane) * 16, 0,
+                                             kCpolSc1);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+      s_last = __hip_atomic_fetch_add(&counters[gi], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               split - 1;
+    __syncthreads();
+    if (!s_last) return;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      u32x4_t part[kSkMaxSplit];
+#pragma unroll
+      for (int c = 0; c < kSkMaxSplit; ++c)
+        if (c < split)
+          part[c] = __builtin_amdgcn_raw_buffer_load_b128(
+              rws, ((c * NW + wave) * MT * 64 + mt * 64 + lane) * 16, 0, kCpolSc1);
+      f32x4_t t = __builtin_bit_cast(f32x4_t, part[0]);
+#pragma unroll
+      for (int c = 1; c < kSkMaxSplit; ++c)
+        if (c < split) t += __builtin_bit_cast(f32x4_t, part[c]);
+      acc[mt] = t;
+    }
+    if (threadIdx.x == 0)
+      __hip_atomic_store(&counters[gi], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (!live) return;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = 16 * mt + r16;
+    if (m >= M || n >= N) continue;
+    float v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float x = acc[mt][r];
+      if (EPI != CGPT_EPI_NONE) x += n + r < N ? bias_value(bias, bias_bf16, n + r) : 0.f;
+      if (EPI == CGPT_EPI_BIAS_GELU) x = gelu_tanh(x);
+      v[r] = x;
+    }
+    TOut* out = C + static_cast<int64_t>(m) * ldc + n;
+    if (vec_store && n + 3 < N) {
+      store4_out(out, v);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (n + r < N) Elem<TOut>::store(out + r, v[r]);
+    }
+  }
+#endif  // __HIP_DEVICE_COMPILE__
 }
 
 static int skinny_num_cus() {
@@ -546,6 +741,127 @@ static bool a_fits(int M, int K, int64_t lda, int es) {
   return static_cast<int64_t>(M - 1) * lda * es + static_cast<int64_t>(K) * es < (int64_t{1} << 31);
 }
 
+// Work split of a decode-form call: `nw` n-tiles (waves) a block, K chunks of
+// `chunk` double slabs in a kernel instance holding `ks` >= chunk, `split`
+// chunks, `groups` column groups.
+struct DecodePlan {
+  int mt, nw, ks, chunk, split, groups;
+  int64_t ws_floats;  // final output with split > 1: every group's chunk sums
+};
+constexpr int kDecKs[] = {2, 3, 5, kDecMaxKs};
+constexpr int kDecChunk = 5;         // double slabs a chunk at most, when the split is ours
+constexpr int kDecWavesPerCu = 5;    // waves (n-tile x chunk units) to aim for a CU
+
+// split > 0: exactly that many K chunks (a partials caller's n_split); 0: chunks
+// of at most kDecChunk double slabs, and more of them while there are fewer
+// than kDecWavesPerCu waves a CU, but at most kSkMaxSplit chunks (the fix-up's
+// limit, and that of the decode step's partials consumers); a chunk that
+// still exceeds kDecChunk takes the longest kernel instance whole.  A sweep of
+// the GPT-2 XL decode shapes on rotated weights picked QKV 5 chunks,
+// projection 13, MLP projection 10 of the choices within 16.  Blocks hold 8
+// waves, or 4 for K of 64 double slabs or more.  nw > 0 forces the waves a
+// block.  False when the shape is not one for the decode form (M > 32, chunks
+// longer than kDecMaxKs, or more than kSkMaxSplit chunks of a final output).
+static bool decode_plan(int M, int N, int K, int split, bool final_out, int nw, DecodePlan* p) {
+  if (M < 1 || M > 32 || N < 1 || K < 1) return false;
+  const int dslabs = (K + 63) / 64;
+  const int tiles = (N + 15) / 16;
+  if (split <= 0) {
+    const int want = (kDecWavesPerCu * skinny_num_cus() + tiles - 1) / tiles;
+    split = std::min({dslabs, kSkMaxSplit, std::max((dslabs + kDecChunk - 1) / kDecChunk, want)});
+    int chunk = (dslabs + split - 1) / split;
+    if (chunk > kDecChunk) chunk = kDecMaxKs;
+    split = (dslabs + chunk - 1) / chunk;
+    if (split > kSkMaxSplit) return false;
+  }
+  if (split > dslabs || (final_out && split > kSkMaxSplit)) return false;
+  const int chunk = (dslabs + split - 1) / split;
+  int ks = 0;
+  for (int k : kDecKs)
+    if (ks == 0 && k >= chunk) ks = k;
+  if (ks == 0) return false;
+  p->mt = M <= 16 ? 1 : 2;
+  p->nw = nw > 0 ? nw : dslabs >= 64 ? 4 : 8;
+  p->ks = ks;
+  p->chunk = chunk;
+  p->split = split;
+  p->groups = (tiles + p->nw - 1) / p->nw;
+  p->ws_floats = final_out && split > 1
+                     ? static_cast<int64_t>(p->groups) * split * p->nw * p->mt * 64 * 4 : 0;
+  return true;
+}
+
+// A final output in the decode form: unsplit when one chunk covers K (a single
+// round trip; the cross-block hand-off costs three more), else split K with
+// the last-block fix-up when there is a workspace.
+static bool decode_final_plan(int M, int N, int K, bool have_ws, DecodePlan* p) {
+  if ((K + 63) / 64 <= kDecMaxKs) return decode_plan(M, N, K, 1, true, 0, p);
+  return have_ws && decode_plan(M, N, K, 0, true, 0, p);
+}
+
+// Both operands' buffer offsets are 32-bit in the decode form (one launch).
+static bool decode_fits(int M, int N, int K, int64_t lda, int64_t ldw) {
+  return a_fits(M, K, lda, 2) && a_fits(N, K, ldw, 2);
+}
+
+template <int MT, int NW, int MODE, int EPI, typename TOut>
+static int launch_decode_nw(const DecodePlan& p, const bf16_t* A, const bf16_t* W, const void* bias,
+                            bool bias_bf16, TOut* C, int M, int N, int K, int lda, int ldw,
+                            int64_t ldc, bool vec_store, float* ws, int* counters, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(p.groups * p.split)), block(64 * NW);
+#define CGPT_DEC(KS)                                                                            \
+  hipLaunchKernelGGL((gemm_decode_kernel<MT, NW, KS, MODE, EPI, TOut>), grid, block, 0, s, A, W, \
+                     bias, bias_bf16, C, M, N, K, lda, ldw, ldc, vec_store, p.split, p.chunk, ws, \
+                     counters)
+  switch (p.ks) {
+    case kDecKs[0]: CGPT_DEC(kDecKs[0]); break;
+    case kDecKs[1]: CGPT_DEC(kDecKs[1]); break;
+    case kDecKs[2]: CGPT_DEC(kDecKs[2]); break;
+    case kDecKs[3]: CGPT_DEC(kDecKs[3]); break;
+    default: return CGPT_EINVAL;
+  }
+#undef CGPT_DEC
+  return hip_status(hipGetLastError());
+}
+
+template <int MODE, int EPI, typename TOut>
+static int launch_decode(const DecodePlan& p, const void* a, const void* w, const void* bias,
+                         bool bias_bf16, void* c, int M, int N, int K, int lda, int ldw, int64_t ldc,
+                         bool vec_store, float* ws, int* counters, hipStream_t s) {
+  const bf16_t* A = static_cast<const bf16_t*>(a);
+  const bf16_t* W = static_cast<const bf16_t*>(w);
+  TOut* C = static_cast<TOut*>(c);
+#define CGPT_DEC_NW(MT, NW)                                                                \
+  return launch_decode_nw<MT, NW, MODE, EPI, TOut>(p, A, W, bias, bias_bf16, C, M, N, K, lda, \
+                                                   ldw, ldc, vec_store, ws, counters, s)
+  if (p.mt == 1) {
+    if (p.nw == 4) CGPT_DEC_NW(1, 4);
+    if (p.nw == 8) CGPT_DEC_NW(1, 8);
+  } else {
+    if (p.nw == 4) CGPT_DEC_NW(2, 4);
+    if (p.nw == 8) CGPT_DEC_NW(2, 8);
+  }
+#undef CGPT_DEC_NW
+  return CGPT_EINVAL;
+}
+
+template <typename TOut>
+static int launch_decode_final(const DecodePlan& p, int epi, const void* a, const void* w,
+                               const void* bias, bool bias_bf16, void* c, int M, int N, int K,
+                               int lda, int ldw, int64_t ldc, bool vec_store, float* ws,
+                               int* counters, hipStream_t s) {
+  switch (epi) {
+    case CGPT_EPI_NONE:
+      return launch_decode<kSkFinal, CGPT_EPI_NONE, TOut>(p, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s);
+    case CGPT_EPI_BIAS:
+      return launch_decode<kSkFinal, CGPT_EPI_BIAS, TOut>(p, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s);
+    case CGPT_EPI_BIAS_GELU:
+      return launch_decode<kSkFinal, CGPT_EPI_BIAS_GELU, TOut>(p, a, w, bias, bias_bf16, c, M, N, K, lda, ldw, ldc, vec_store, ws, counters, s);
+    default:
+      return CGPT_EINVAL;
+  }
+}
+
 int launch_gemm_skinny(bool bf16_in, int epilogue, const void* a, const void* w, const void* bias,
                        bool bias_bf16, void* c, bool out_bf16, int M, int N, int K, int64_t lda,
                        int64_t ldw, int64_t ldc, void* workspace, int64_t ws_bytes, int* counters,
@@ -560,6 +876,19 @@ int launch_gemm_skinny(bool bf16_in, int epilogue, const void* a, const void* w,
     const int li = static_cast<int>(lda), lw = static_cast<int>(ldw);
     return out_bf16 ? launch_wide<bf16_t>(epilogue, a, w, bias, bias_bf16, c, M, N, K, li, lw, ldc, vec_store, s)
                     : launch_wide<float>(epilogue, a, w, bias, bias_bf16, c, M, N, K, li, lw, ldc, vec_store, s);
+  }
+  // The decode form, when its split (if any) fits the workspace given.
+  DecodePlan dp;
+  if (bf16_in && decode_fits(M, N, K, lda, ldw) && decode_final_plan(M, N, K, have_ws, &dp) &&
+      (dp.split == 1 || (dp.ws_floats * 4 <= ws_bytes && dp.groups <= n_counters &&
+                         (reinterpret_cast<uintptr_t>(workspace) & 15) == 0))) {
+    const uintptr_t oa = out_bf16 ? 7 : 15;
+    const bool vec_store = ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(c) & oa) == 0;
+    const int li = static_cast<int>(lda), lw = static_cast<int>(ldw);
+    float* wsf = dp.split > 1 ? static_cast<float*>(workspace) : nullptr;
+    int* cnt = dp.split > 1 ? counters : nullptr;
+    return out_bf16 ? launch_decode_final<bf16_t>(dp, epilogue, a, w, bias, bias_bf16, c, M, N, K, li, lw, ldc, vec_store, wsf, cnt, s)
+                    : launch_decode_final<float>(dp, epilogue, a, w, bias, bias_bf16, c, M, N, K, li, lw, ldc, vec_store, wsf, cnt, s);
   }
   const SkinnyPlan p = skinny_plan(M, N, K, es, have_ws);
   const int scols = 16 * kSkShapes[p.shape].nt;
@@ -597,14 +926,23 @@ int launch_gemm_skinny(bool bf16_in, int epilogue, const void* a, const void* w,
   return CGPT_OK;
 }
 
+// Enough for either form (the decode form runs when the workspace holds its
+// split; the other split-K form otherwise).
 int skinny_workspace(int M, int N, int K, bool bf16_in, int64_t* ws_bytes, int64_t* n_counters) {
   const SkinnyPlan p = skinny_plan(M, N, K, bf16_in ? 2 : 4, true);
   *ws_bytes = p.ws_floats * 4;
   *n_counters = p.split > 1 ? p.slices : 0;
+  DecodePlan dp;
+  if (bf16_in && decode_final_plan(M, N, K, true, &dp) && dp.split > 1) {
+    *ws_bytes = std::max(*ws_bytes, dp.ws_floats * 4);
+    *n_counters = std::max(*n_counters, static_cast<int64_t>(dp.groups));
+  }
   return CGPT_OK;
 }
 
 int gemm_partials_split(int M, int N, int K, bool bf16_in) {
+  DecodePlan dp;
+  if (bf16_in && decode_plan(M, N, K, 0, false, 0, &dp)) return dp.split;
   return partials_plan(M, N, K, bf16_in ? 2 : 4, 0).split;
 }
 
@@ -614,6 +952,13 @@ int launch_gemm_partials(bool bf16_in, const void* a, const void* w, float* part
   const int es = bf16_in ? 2 : 4;
   const SkinnyPlan p = partials_plan(M, N, K, es, split);
   if (split < 1 || split > p.dslabs) return CGPT_EINVAL;
+  DecodePlan dp;
+  if (bf16_in && decode_fits(M, N, K, lda, ldw) && decode_plan(M, N, K, split, false, 0, &dp)) {
+    const bool vec_store = ldp % 4 == 0 && (reinterpret_cast<uintptr_t>(partials) & 15) == 0;
+    return launch_decode<kSkPartials, CGPT_EPI_NONE, float>(
+        dp, a, w, nullptr, false, partials, M, N, K, static_cast<int>(lda), static_cast<int>(ldw),
+        ldp, vec_store, nullptr, nullptr, s);
+  }
   const int scols = 16 * kSkShapes[p.shape].nt;
   const int step = cols_per_launch(N, K, ldw, es, scols);
   if (step == 0 || !a_fits(M, K, lda, es)) return CGPT_ESHAPE;
