@@ -66,6 +66,8 @@ SIGNATURES = {
     "cgpt_kv_store": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
                            _I64, _I64, _I64, _I64, _I64, _I64, _I, _P]),
     "cgpt_argmax": (_I, [_P, _I64, _I64, _I64, _I, _P, _P, _I64, _P, _P]),
+    "cgpt_partials_bias_act": (_I, [_P, _I64, _I64, _I64, _P, _I, _P, _I64, _I64, _I64, _I, _I,
+                                    _P]),
 }
 
 ABI_VERSION = 1

@@ -409,6 +409,72 @@ static int launch_decode(const DecIn<T>& in, int maxp, void* k_cache, void* v_ca
   return hip_status(hipGetLastError());
 }
 
+// ------------------------------------------- split-K partials + bias + GELU
+
+// out[r][c..c+3] = act(P[0] + ... + P[n-1] + bias) for one 4-column group a
+// thread: all MAXP partial vectors are loaded before the first is added
+// (slots past n lie past the record count and read as zero; adding +0 leaves
+// every sum but -0 as is, and the sum starts from P[0]), fp32 additions in
+// chunk order, then the bias, the activation and one rounding — the values
+// the GEMM's own bias / GELU epilogue stores.
+template <int MAXP, bool BIAS_BF16, bool GELU, typename TOut>
+__global__ __launch_bounds__(256) void partials_bias_act_kernel(
+    const float* __restrict__ P, int n_parts, int part_stride, int ldp, const void* __restrict__ bias,
+    TOut* __restrict__ out, int64_t ldo, int rows, int cols) {
+  const int groups = cols / 4;
+  const int i = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+  if (i >= rows * groups) return;
+  const int r = i / groups, c = (i - r * groups) * 4;
+  const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(P), 0, n_parts * part_stride * 4, 0x00020000);
+  const uint32_t off = static_cast<uint32_t>(r * ldp + c) * 4;
+  u32x4_t pv[MAXP];
+#pragma unroll
+  for (int s = 0; s < MAXP; ++s)
+    pv[s] = __builtin_amdgcn_raw_buffer_load_b128(
+        rp, s < n_parts ? off + static_cast<uint32_t>(s * part_stride) * 4 : 0x80000000u, 0, 0);
+  float b[4];
+  if constexpr (BIAS_BF16) {
+    const u32x2_t w = *reinterpret_cast<const u32x2_t*>(static_cast<const bf16_t*>(bias) + c);
+    b[0] = __uint_as_float(w[0] << 16);
+    b[1] = __uint_as_float(w[0] & 0xffff0000u);
+    b[2] = __uint_as_float(w[1] << 16);
+    b[3] = __uint_as_float(w[1] & 0xffff0000u);
+  } else {
+    const u32x4_t w = *reinterpret_cast<const u32x4_t*>(static_cast<const float*>(bias) + c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) b[e] = __uint_as_float(w[e]);
+  }
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float t = __uint_as_float(pv[0][e]);
+#pragma unroll
+    for (int s = 1; s < MAXP; ++s) t += __uint_as_float(pv[s][e]);
+    t += b[e];
+    v[e] = GELU ? gelu_tanh(t) : t;
+  }
+  store4_out(out + static_cast<int64_t>(r) * ldo + c, v);
+}
+
+template <int MAXP, bool GELU>
+static int launch_pba_maxp(const float* P, int n, int ps, int ldp, const void* bias, bool bias_bf16,
+                           void* out, bool out_bf16, int64_t ldo, int rows, int cols,
+                           hipStream_t s) {
+  const int threads = rows * (cols / 4);
+  const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+#define CGPT_PBA(BB, TO)                                                                           \
+  hipLaunchKernelGGL((partials_bias_act_kernel<MAXP, BB, GELU, TO>), grid, dim3(256), 0, s, P, n, \
+                     ps, ldp, bias, static_cast<TO*>(out), ldo, rows, cols)
+  if (bias_bf16) {
+    if (out_bf16) CGPT_PBA(true, bf16_t); else CGPT_PBA(true, float);
+  } else {
+    if (out_bf16) CGPT_PBA(false, bf16_t); else CGPT_PBA(false, float);
+  }
+#undef CGPT_PBA
+  return hip_status(hipGetLastError());
+}
+
 }  // namespace cgpt
 
 using namespace cgpt;
@@ -521,4 +587,36 @@ extern "C" int cgpt_argmax(const void* x, int64_t rows, int64_t cols, int64_t ld
   else
     return CGPT_EDTYPE;
   return hip_status(hipGetLastError());
+}
+
+extern "C" int cgpt_partials_bias_act(const float* partials, int64_t n_parts, int64_t part_stride,
+                                      int64_t ldp, const void* bias, int bias_dtype, void* out,
+                                      int64_t ldo, int64_t rows, int64_t cols, int epilogue,
+                                      int out_dtype, void* stream) {
+  if (rows < 0 || cols < 0) return CGPT_EINVAL;
+  if (rows == 0 || cols == 0) return CGPT_OK;
+  if (partials == nullptr || bias == nullptr || out == nullptr) return CGPT_EINVAL;
+  if (epilogue != CGPT_EPI_BIAS && epilogue != CGPT_EPI_BIAS_GELU) return CGPT_EINVAL;
+  if ((bias_dtype != CGPT_F32 && bias_dtype != CGPT_BF16) ||
+      (out_dtype != CGPT_F32 && out_dtype != CGPT_BF16))
+    return CGPT_EDTYPE;
+  if (n_parts < 1 || n_parts > 16 || cols % 4 != 0 || ldp < cols || ldp % 4 != 0 ||
+      part_stride % 4 != 0 || part_stride < (rows - 1) * ldp + cols || ldo < cols || ldo % 4 != 0)
+    return CGPT_EINVAL;
+  const uintptr_t ba = bias_dtype == CGPT_F32 ? 15 : 7, oa = out_dtype == CGPT_F32 ? 15 : 7;
+  if ((reinterpret_cast<uintptr_t>(partials) & 15) || (reinterpret_cast<uintptr_t>(bias) & ba) ||
+      (reinterpret_cast<uintptr_t>(out) & oa))
+    return CGPT_EINVAL;
+  if (n_parts * part_stride * 4 >= (int64_t{1} << 31) || rows * (cols / 4) > 0x7fffffff)
+    return CGPT_ESHAPE;
+  const int n = static_cast<int>(n_parts), ps = static_cast<int>(part_stride);
+  const int lp = static_cast<int>(ldp), r = static_cast<int>(rows), c = static_cast<int>(cols);
+  const bool bb = bias_dtype == CGPT_BF16, ob = out_dtype == CGPT_BF16;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool gelu = epilogue == CGPT_EPI_BIAS_GELU;
+  if (n <= 8)
+    return gelu ? launch_pba_maxp<8, true>(partials, n, ps, lp, bias, bb, out, ob, ldo, r, c, s)
+                : launch_pba_maxp<8, false>(partials, n, ps, lp, bias, bb, out, ob, ldo, r, c, s);
+  return gelu ? launch_pba_maxp<16, true>(partials, n, ps, lp, bias, bb, out, ob, ldo, r, c, s)
+              : launch_pba_maxp<16, false>(partials, n, ps, lp, bias, bb, out, ob, ldo, r, c, s);
 }

@@ -12,7 +12,8 @@ and every further token costs one step over B rows:
                                      partials + bias, appends k, v at pos)
                proj GEMM             cgpt_gemm_partials
                residual + LN_2       cgpt_add_layernorm_partials
-               fc + GELU             cgpt_gemm (skinny, M = B)
+               fc GEMM               cgpt_gemm_partials
+               bias + GELU           cgpt_partials_bias_act (adds the partials)
                MLP proj GEMM         cgpt_gemm_partials
                residual + next LN    cgpt_add_layernorm_partials (LN_f last)
     LM head                          cgpt_gemm (skinny, N = vocab)
@@ -94,7 +95,7 @@ class DecodeSession:
         self.partials = partials
         self.splits = {}
         p_max = 4
-        for n, k in ((3 * D, D), (D, D), (D, 4 * D)):
+        for n, k in ((3 * D, D), (D, D), (4 * D, D), (D, 4 * D)):
             ns = ctypes.c_int64()
             _lib.check(lib.cgpt_gemm_partials_plan(B, n, k, _DT[act], ctypes.byref(ns)), "partials plan")
             self.splits[(n, k)] = ns.value
@@ -200,8 +201,13 @@ class DecodeSession:
                     "attention_decode_partials")
                 ns = gemm_parts(pa, W[p + "attn.c_proj.weight"], D, D)
                 add_ln_parts(ns, W[p + "attn.c_proj.bias"], p + "ln_2")
-                gemm(ph, W[p + "mlp.c_fc.weight"], W[p + "mlp.c_fc.bias"], pf, 4 * D, D,
-                     _lib.EPI_BIAS_GELU, ac, split=False)
+                # c_fc as split-K partials, then bias + GELU in one pass over them
+                # (the GEMM's own fix-up would cost three dependent round trips).
+                ns = gemm_parts(ph, W[p + "mlp.c_fc.weight"], 4 * D, D)
+                chk(lib.cgpt_partials_bias_act(pp, ns, B * 4 * D, 4 * D,
+                                               W[p + "mlp.c_fc.bias"].data_ptr(), ac, pf, 4 * D,
+                                               B, 4 * D, _lib.EPI_BIAS_GELU, ac, s),
+                    "partials_bias_act")
                 ns = gemm_parts(pf, W[p + "mlp.c_proj.weight"], D, 4 * D)
                 add_ln_parts(ns, W[p + "mlp.c_proj.bias"], ln_next, keep_x=not last)
                 continue

@@ -107,6 +107,24 @@ int cgpt_add_layernorm_partials(const void* x, const float* partials, int64_t n_
                                 int param_dtype, int y_dtype, void* stream);
 
 /*
+ * The consumer of a split-K cgpt_gemm_partials whose output takes a bias and
+ * an activation: out[r][c] = act(P[0][r][c] + ... + P[n_parts-1][r][c] +
+ * bias[c]), the sums in fp32 in that order, rounded once to out_dtype — the
+ * values the GEMM's own bias / GELU epilogue stores.  epilogue:
+ * CGPT_EPI_BIAS (no activation) or CGPT_EPI_BIAS_GELU (tanh GELU).  P[s] row r
+ * at partials + s * part_stride + r * ldp floats (16-byte aligned; ldp,
+ * part_stride multiples of 4); 1 <= n_parts <= 16; cols % 4 == 0; bias of
+ * bias_dtype, out of out_dtype (fp32 or bf16; 16- / 8-byte aligned), rows of
+ * ldo >= cols elements, ldo % 4 == 0.  Replaces cutile_linear_bias +
+ * cutile_gelu on the MLP up-projection at decode shapes
+ * (cutile_gpt/models/gpt.py:161-167, kernels/linear.py:112-222,
+ * kernels/gelu.py:20-41).
+ */
+int cgpt_partials_bias_act(const float* partials, int64_t n_parts, int64_t part_stride,
+                           int64_t ldp, const void* bias, int bias_dtype, void* out, int64_t ldo,
+                           int64_t rows, int64_t cols, int epilogue, int out_dtype, void* stream);
+
+/*
  * C[M,N] = epilogue(A[M,K] * W[N,K]^T (+ bias[N])).
  * A row-major with leading dimension lda, W row-major (out_features, in_features)
  * with leading dimension ldw — the nn.Linear / cutileGPT `weight` layout, so no

@@ -1,6 +1,6 @@
 """Decode-step kernels that hand a GEMM's split-K reduction to its consumer:
-cgpt_gemm_partials, cgpt_add_layernorm_partials and
-cgpt_attention_decode_partials.
+cgpt_gemm_partials, cgpt_add_layernorm_partials,
+cgpt_attention_decode_partials and cgpt_partials_bias_act.
 
 The partial products are pinned against fp64 products of the K chunks they
 cover; the consumers are pinned against the direct-input kernels fed with the
@@ -237,6 +237,98 @@ def test_attention_decode_partials_rejects_bad_args(gpu):
     assert call(ps=3 * D) == -1            # slices overlap
     assert call(v_off=3 * D) == -1
     assert call(bias=None) == -1
+
+
+# --------------------------------------------------- bias + activation consumer
+
+def _pba(lib, gpu, parts, S, rows, cols, ldp, bias, out, ldo, epi, out_dtype):
+    return lib.cgpt_partials_bias_act(parts.data_ptr(), S, rows * ldp, ldp, bias.data_ptr(),
+                                      DT[bias.dtype], out.data_ptr(), ldo, rows, cols, epi,
+                                      DT[out_dtype], stream(gpu))
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("bias_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("rows,cols,S", [(32, 6400, 5), (3, 100, 1), (64, 768, 16), (5, 4096, 9),
+                                         (1, 4, 8)])
+def test_partials_bias_act_matches_host_reduction(gpu, out_dtype, bias_dtype, rows, cols, S):
+    """Bias only: bit-identical to the in-order host sum (fp32 additions are
+    exact IEEE operations) rounded once.  GELU: within one rounding (plus the
+    fp32 GELU's own error) of the fp64 GELU of that same fp32 sum.  Padding
+    of the output rows untouched."""
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(rows * 7 + cols + S)
+    ldp, ldo = cols + 4, cols + 8
+    parts = torch.randn(S, rows, ldp, generator=g).to(gpu)
+    bias = torch.randn(cols, generator=g).to(bias_dtype).to(gpu)
+    t = reduce_in_order(parts[:, :, :cols], bias)  # fp32, P[0] + ... + P[S-1] + bias
+    for epi in (_lib.EPI_BIAS, _lib.EPI_BIAS_GELU):
+        out = torch.full((rows, ldo), float("nan"), device=gpu).to(out_dtype)
+        _lib.check(_pba(lib, gpu, parts, S, rows, cols, ldp, bias, out, ldo, epi, out_dtype), "pba")
+        torch.cuda.synchronize()
+        assert torch.isnan(out[:, cols:].float()).all()
+        got = out[:, :cols]
+        if epi == _lib.EPI_BIAS:
+            assert torch.equal(got, t.to(out_dtype))
+        else:
+            ref = R.gelu_tanh(t.double())
+            err = (got.double() - ref).abs() / (ref.abs() + 1e-3)
+            # bf16: one rounding (half an ulp, 2^-8 relative) over the fp32
+            # GELU's few-ulp error (x / (1 + exp2(.)) on the hardware exp2 and
+            # reciprocal); fp32: that error alone.
+            tol = 2 ** -8 + 4e-6 if out_dtype == torch.bfloat16 else 4e-6
+            assert err.max().item() <= tol, err.max().item()
+
+
+def test_partials_bias_act_agrees_with_gemm_epilogue(gpu):
+    """cgpt_gemm_partials + cgpt_partials_bias_act against the skinny GEMM's own
+    bias + GELU epilogue on the same operands (fp32 summation order only)."""
+    lib = _lib.load()
+    M, N, K = 32, 6400, 1600
+    g = torch.Generator().manual_seed(5)
+    a = torch.randn(M, K, generator=g).bfloat16().to(gpu)
+    w = (torch.randn(N, K, generator=g) * 0.05).bfloat16().to(gpu)
+    b = (torch.randn(N, generator=g) * 0.1).bfloat16().to(gpu)
+    S = plan(lib, M, N, K, torch.bfloat16)
+    p = torch.empty(S, M, N, device=gpu)
+    _lib.check(lib.cgpt_gemm_partials(a.data_ptr(), w.data_ptr(), p.data_ptr(), M, N, K, K, K, N, S,
+                                      _lib.CGPT_BF16, stream(gpu)), "partials")
+    out = torch.empty(M, N, device=gpu)
+    _lib.check(_pba(lib, gpu, p, S, M, N, N, b, out, N, _lib.EPI_BIAS_GELU, torch.float32), "pba")
+    ref = torch.empty(M, N, device=gpu)
+    _lib.check(lib.cgpt_gemm_skinny(a.data_ptr(), w.data_ptr(), b.data_ptr(), ref.data_ptr(), M, N,
+                                    K, K, K, N, _lib.CGPT_BF16, _lib.CGPT_BF16, _lib.CGPT_F32,
+                                    _lib.EPI_BIAS_GELU, None, 0, None, 0, stream(gpu)), "skinny")
+    torch.cuda.synchronize()
+    exact = R.gelu_tanh(a.double() @ w.double().t() + b.double())
+    assert (out.double() - exact).abs().max().item() <= 1e-4
+    assert (out - ref).abs().max().item() <= 1e-4
+
+
+def test_partials_bias_act_rejects_bad_args(gpu):
+    lib = _lib.load()
+    rows, cols, S = 4, 64, 3
+    parts = torch.zeros(S, rows, cols, device=gpu)
+    bias = torch.zeros(cols, device=gpu)
+    out = torch.empty(rows, cols, device=gpu)
+
+    def call(S=S, ps=rows * cols, ldp=cols, b=bias, bdt=_lib.CGPT_F32, o=out.data_ptr(),
+             ldo=cols, c=cols, epi=_lib.EPI_BIAS_GELU, odt=_lib.CGPT_F32, p=parts.data_ptr()):
+        return lib.cgpt_partials_bias_act(p, S, ps, ldp, None if b is None else b.data_ptr(), bdt,
+                                          o, ldo, rows, c, epi, odt, stream(gpu))
+
+    assert call() == 0
+    assert call(S=0) == -1 and call(S=17) == -1
+    assert call(c=62, ldp=62, ldo=62) == -1       # cols % 4
+    assert call(ldp=cols - 4) == -1
+    assert call(ps=(rows - 1) * cols) == -1       # slices overlap
+    assert call(ldo=cols - 4) == -1
+    assert call(b=None) == -1
+    assert call(epi=_lib.EPI_NONE) == -1
+    assert call(odt=_lib.CGPT_F16) == -2
+    assert call(p=parts.data_ptr() + 4) == -1     # partials 16-byte aligned
+    assert call(o=out.data_ptr() + 4) == -1       # fp32 output 16-byte aligned
+    torch.cuda.synchronize()
 
 
 # ------------------------------------------------------------------ decode step
