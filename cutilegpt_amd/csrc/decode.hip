@@ -108,13 +108,14 @@ __global__ __launch_bounds__(kDecThreads, NV <= 8 ? 4 : 1) void attn_decode_kern
                                 : in.vn + b * in.vn_sb + h * in.vn_sh;
       sv[r] = Elem<T>::load(src + d);  // threads past 3 * HD load a valid element, unused
     } else {
-      // Partials past n_parts lie past the record count and read as zero.
+      // Partials past n_parts (a uniform branch: no load issued) hold +0.
       const int64_t col = (which == 0 ? in.q_off : which == 1 ? in.k_off : in.v_off) + h * HD + d;
       const uint32_t off = static_cast<uint32_t>((b * in.ldp + col) * 4);
 #pragma unroll
       for (int s = 0; s < MAXP; ++s)
-        pv[r][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-            rp, s < in.n_parts ? off + static_cast<uint32_t>(s * in.part_stride * 4) : 0x80000000u, 0, 0));
+        pv[r][s] = s < in.n_parts ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                                        rp, off + static_cast<uint32_t>(s * in.part_stride * 4), 0, 0))
+                                  : 0.f;
       bv[r] = Elem<T>::load(in.bias + col);
     }
   }
@@ -412,9 +413,9 @@ static int launch_decode(const DecIn<T>& in, int maxp, void* k_cache, void* v_ca
 // ------------------------------------------- split-K partials + bias + GELU
 
 // out[r][c..c+3] = act(P[0] + ... + P[n-1] + bias) for one 4-column group a
-// thread: all MAXP partial vectors are loaded before the first is added
-// (slots past n lie past the record count and read as zero; adding +0 leaves
-// every sum but -0 as is, and the sum starts from P[0]), fp32 additions in
+// thread: the n partial vectors are all loaded before the first is added
+// (slots past n, skipped by a uniform branch, hold +0; adding +0 leaves every
+// sum but -0 as is, and the sum starts from P[0]), fp32 additions in
 // chunk order, then the bias, the activation and one rounding — the values
 // the GEMM's own bias / GELU epilogue stores.
 template <int MAXP, bool BIAS_BF16, bool GELU, typename TOut>
@@ -431,8 +432,9 @@ __global__ __launch_bounds__(256) void partials_bias_act_kernel(
   u32x4_t pv[MAXP];
 #pragma unroll
   for (int s = 0; s < MAXP; ++s)
-    pv[s] = __builtin_amdgcn_raw_buffer_load_b128(
-        rp, s < n_parts ? off + static_cast<uint32_t>(s * part_stride) * 4 : 0x80000000u, 0, 0);
+    pv[s] = s < n_parts ? __builtin_amdgcn_raw_buffer_load_b128(
+                              rp, off + static_cast<uint32_t>(s * part_stride) * 4, 0, 0)
+                        : u32x4_t{0u, 0u, 0u, 0u};
   float b[4];
   if constexpr (BIAS_BF16) {
     const u32x2_t w = *reinterpret_cast<const u32x2_t*>(static_cast<const bf16_t*>(bias) + c);

@@ -524,11 +524,12 @@ __global__ __launch_bounds__(kLnpThreads) void add_layernorm_partials_kernel(
     const int col = (c * kLnpThreads + tid) * 4;
     const int cc = col < cols ? col : 0;
     load4(x + base + cc, v[c]);
+    // Slots past n_parts (a uniform branch: no load issued) hold +0.
 #pragma unroll
     for (int s = 0; s < MAXP; ++s)
-      praw[c][s] = __builtin_amdgcn_raw_buffer_load_b128(
-          rp, s < n_parts ? static_cast<uint32_t>(((s * part_stride) + row * ldp + cc) * 4) : 0x80000000u,
-          0, 0);
+      praw[c][s] = s < n_parts ? __builtin_amdgcn_raw_buffer_load_b128(
+                                     rp, static_cast<uint32_t>(((s * part_stride) + row * ldp + cc) * 4), 0, 0)
+                               : u32x4_t{0u, 0u, 0u, 0u};
     graw[c] = __builtin_amdgcn_raw_buffer_load_b128(rg, cc << pshift, 0, 0);
     braw[c] = __builtin_amdgcn_raw_buffer_load_b128(rb, cc << pshift, 0, 0);
     biraw[c] = __builtin_amdgcn_raw_buffer_load_b128(rbi, cc << pshift, 0, 0);
