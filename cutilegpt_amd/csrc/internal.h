@@ -30,6 +30,11 @@ int launch_gemm_skinny(bool bf16_in, int epilogue, const void* a, const void* w,
 // Workspace bytes and counters the split-K skinny GEMM uses for (M, N, K).
 int skinny_workspace(int M, int N, int K, bool bf16_in, int64_t* ws_bytes, int64_t* n_counters);
 
+// Every split-K plan launch_gemm_skinny makes stays within these (the
+// no-allocation entry point's static scratch has exactly this capacity).
+constexpr int64_t kSkinnyMaxWsBytes = int64_t{8} << 20;
+constexpr int kSkinnyMaxCounters = 1024;
+
 // Split-K partial products P[s][m][n] (fp32, P[s] at partials + s * M * ldp)
 // of the skinny GEMM, for a consumer that adds them; the split the kernel is
 // tuned for, and the launch.

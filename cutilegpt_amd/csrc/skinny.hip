@@ -793,10 +793,13 @@ static bool decode_plan(int M, int N, int K, int split, bool final_out, int nw, 
 
 // A final output in the decode form: unsplit when one chunk covers K (a single
 // round trip; the cross-block hand-off costs three more), else split K with
-// the last-block fix-up when there is a workspace.
+// the last-block fix-up when there is a workspace and the split's chunk sums
+// and counters fit kSkinnyMaxWsBytes / kSkinnyMaxCounters.
 static bool decode_final_plan(int M, int N, int K, bool have_ws, DecodePlan* p) {
   if ((K + 63) / 64 <= kDecMaxKs) return decode_plan(M, N, K, 1, true, 0, p);
-  return have_ws && decode_plan(M, N, K, 0, true, 0, p);
+  // Beyond the scratch capacity every split plan keeps to, the other form.
+  return have_ws && decode_plan(M, N, K, 0, true, 0, p) &&
+         p->ws_floats * 4 <= kSkinnyMaxWsBytes && p->groups <= kSkinnyMaxCounters;
 }
 
 // Both operands' buffer offsets are 32-bit in the decode form (one launch).

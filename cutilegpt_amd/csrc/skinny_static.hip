@@ -19,9 +19,11 @@ namespace cgpt {
 // Capacity.  The skinny planner splits K only while it has fewer than 512
 // column slices, with at most 16 chunks a slice, so slices * split < 1024 and
 // the partial tiles of a call take at most 1023 * 4 m-tiles * 2 n-tiles * 256
-// floats = 8 MiB - 8 KiB; counters: one per slice, at most 511.
-constexpr int64_t kScratchWsBytes = int64_t{8} << 20;
-constexpr int kScratchCounters = 1024;
+// floats = 8 MiB - 8 KiB; counters: one per slice, at most 511.  The
+// decode-form split is taken only when its chunk sums and counters fit the
+// same capacity (else the other form runs).
+constexpr int64_t kScratchWsBytes = kSkinnyMaxWsBytes;
+constexpr int kScratchCounters = kSkinnyMaxCounters;
 constexpr int64_t kScratchBytes = kScratchWsBytes + kScratchCounters * 4;
 
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];

@@ -87,6 +87,23 @@ def test_noalloc_largest_split_fits(gpu):
     assert torch.equal(out, ref)
 
 
+@pytest.mark.parametrize("N", [16352, 30000])
+def test_noalloc_decode_form_within_capacity(gpu, N):
+    """32 bf16 rows, K = 1024: the decode form's split (4 chunks, 8 n-tiles a
+    block) needs exactly 8 MiB of chunk sums at N = 16352 and is taken; at
+    N = 30000 it would need 15 MB, so both entry points take the other form
+    instead — the workspace query stays within the static array and the two
+    paths stay bit-identical."""
+    out, ref, n_counters, ws_bytes = _run_pair(gpu, 32, N, 1024, _lib.EPI_BIAS,
+                                               torch.bfloat16, torch.float32)
+    assert ws_bytes <= 8 << 20 and n_counters <= 1024
+    assert torch.isfinite(out).all()
+    assert torch.equal(out, ref)
+    a, w, b = _operands(gpu, 32, N, 1024, torch.bfloat16)
+    exact = a.double() @ w.double().t() + b.double()
+    assert (out.double() - exact).abs().max().item() <= 1e-4 * (exact.abs().max().item() + 1)
+
+
 def test_noalloc_graph_capture_and_no_device_allocation(gpu):
     """The call captured in a HIP graph and replayed three times, with other
     work and synchronisations between the replays, gives the eager
