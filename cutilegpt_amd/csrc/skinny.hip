@@ -943,10 +943,11 @@ int skinny_workspace(int M, int N, int K, bool bf16_in, int64_t* ws_bytes, int64
   return CGPT_OK;
 }
 
+// At most kSkMaxSplit chunks: the decode step's consumers add up to 16.
 int gemm_partials_split(int M, int N, int K, bool bf16_in) {
   DecodePlan dp;
   if (bf16_in && decode_plan(M, N, K, 0, false, 0, &dp)) return dp.split;
-  return partials_plan(M, N, K, bf16_in ? 2 : 4, 0).split;
+  return std::min(partials_plan(M, N, K, bf16_in ? 2 : 4, 0).split, kSkMaxSplit);
 }
 
 int launch_gemm_partials(bool bf16_in, const void* a, const void* w, float* partials, int M, int N,

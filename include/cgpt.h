@@ -224,7 +224,8 @@ int cgpt_gemm_partials(const void* a, const void* w, float* partials, int64_t M,
                        int64_t K, int64_t lda, int64_t ldw, int64_t ldp, int64_t n_split,
                        int in_dtype, void* stream);
 
-/* The n_split cgpt_gemm_partials is tuned for at (M, N, K, in_dtype). */
+/* The n_split cgpt_gemm_partials is tuned for at (M, N, K, in_dtype); at most 16,
+ * the most the partials consumers take. */
 int cgpt_gemm_partials_plan(int64_t M, int64_t N, int64_t K, int in_dtype, int64_t* n_split);
 
 /*

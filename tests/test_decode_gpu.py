@@ -334,6 +334,30 @@ def test_decode_logits_match_full_forward(gpu, dtype):
     assert sess.err.item() == 0 and sess.step.item() == n - 1
 
 
+def test_decode_fp32_at_xl_width(gpu):
+    """fp32 decode at GPT-2 XL's width (d 1600, 25 heads, 2 layers, batch 32):
+    the MLP projection's K = 6400 would take 20 split-K chunks at the fp32
+    slab width, more than the 16 partials the consumers add, so the planner
+    caps it; every step's logits still match the full forward."""
+    m, _, cfg = small_model(torch.float32, n_layer=2, n_head=25, n_embd=1600, seed=7)
+    B, T0, n = 32, 5, 4
+    idx = torch.randint(0, cfg.vocab_size, (B, T0), generator=torch.Generator().manual_seed(9)).to(gpu)
+    sess = DecodeSession(m, B, T0, n)
+    sess.prefill(idx)
+    seen = [sess.logits.float().clone()]
+    sess.greedy_first()
+    for _ in range(n - 1):
+        sess.greedy_step()
+        seen.append(sess.logits.float().clone())
+    torch.cuda.synchronize()
+    assert sess.err.item() == 0
+    full, _ = m.forward(torch.cat([idx, sess.hist], dim=1))
+    for s, lg in enumerate(seen):
+        e = (lg - full[:, T0 - 1 + s, :].float()).abs().max().item()
+        assert e <= 1e-3, (s, e)
+        assert torch.equal(sess.hist[:, s], lg.argmax(-1))
+
+
 def test_greedy_graph_replay_equals_eager(gpu):
     """Replaying the captured step gives exactly the eager tokens (every
     replay is checked through the history it writes)."""

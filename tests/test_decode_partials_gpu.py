@@ -82,6 +82,17 @@ def test_gemm_partials_chunks_vs_fp64(gpu, dtype, M, N, K):
         assert (pc[:S, :, :N].sum(0) - tot).abs().max().item() <= 2e-5 * scale * S
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("M,N,K", [(32, 1600, 6400), (32, 6400, 1600), (64, 1024, 4096),
+                                   (8, 768, 3072), (32, 1280, 5120)])
+def test_gemm_partials_plan_fits_the_consumers(gpu, dtype, M, N, K):
+    """The planned split never exceeds the 16 partials the decode step's
+    consumers add (fp32 at K = 6400 alone would take 20 chunks of 10)."""
+    lib = _lib.load()
+    dslabs = -(-K // kd(dtype))
+    assert 1 <= plan(lib, M, N, K, dtype) <= min(16, dslabs)
+
+
 def test_gemm_partials_unaligned_output_and_limits(gpu):
     lib = _lib.load()
     M, N, K = 7, 30, 128
