@@ -421,10 +421,30 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4,
 
   // DMA of block j into stage buffer `buf`: instruction ii of this wave
   // fills rows (ii * NWAVE + wave) * RPI + lane / CPR; keys past Tk re-read
-  // the last key (masked later).
+  // the last key (masked later).  When K and V share a row stride (always
+  // for the fused QKV output), a block wholly below Tk adds its uniform key
+  // offset kv0 * stride through the instruction's SGPR offset to the lane's
+  // loop-invariant row part, so issuing it takes no VALU work.
   const int lrow = lane / CPR, slot = lane % CPR;
+  const bool same_st = k_st == v_st;
+  uint32_t kvo[INS];
+#pragma unroll
+  for (int ii = 0; ii < INS; ++ii) {
+    const int row = (ii * NWAVE + wave) * RPI + lrow;
+    kvo[ii] = static_cast<uint32_t>(row * k_st * 2) + static_cast<uint32_t>((slot ^ (row & 7)) << 4);
+  }
   auto issue = [&](int j, uint8_t* buf) {
     const int kv0 = j * BKV;
+    if (same_st && kv0 + BKV <= Tk) {
+      const uint32_t so = static_cast<uint32_t>(kv0 * k_st * 2);
+#pragma unroll
+      for (int ii = 0; ii < INS; ++ii) {
+        const uint32_t lds = (ii * NWAVE + wave) * 1024;
+        dma_lds16(rk, lds_addr(buf + lds), kvo[ii], so);
+        dma_lds16(rv, lds_addr(buf + XB + lds), kvo[ii], so);
+      }
+      return;
+    }
 #pragma unroll
     for (int ii = 0; ii < INS; ++ii) {
       const int row = (ii * NWAVE + wave) * RPI + lrow;
