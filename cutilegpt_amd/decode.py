@@ -64,6 +64,12 @@ class DecodeSession:
     """Buffers, cache and device counters of one batched generation."""
 
     def __init__(self, model, B: int, t0: int, max_new: int, partials: bool = True):
+        # Ordinary (not inference-mode) tensors even when created inside
+        # generate(): the session and its graphs outlive the call.
+        with torch.inference_mode(False):
+            self._init(model, B, t0, max_new, partials)
+
+    def _init(self, model, B: int, t0: int, max_new: int, partials: bool) -> None:
         cfg = model.config
         if t0 + max_new > cfg.block_size:
             raise ValueError(f"prompt {t0} + {max_new} new tokens exceeds block_size {cfg.block_size}")
@@ -86,7 +92,11 @@ class DecodeSession:
         self.f = torch.empty((B, 4 * D), dtype=act, device=dev)
         self.logits = torch.empty((B, V), dtype=model.logits_dtype, device=dev)
         self.err = torch.zeros(1, dtype=torch.int32, device=dev)
+        # Captured greedy step and logits step, and the weight tensors they
+        # were captured over (a graph holds device pointers).
         self.graph: Optional[torch.cuda.CUDAGraph] = None
+        self.graph_logits: Optional[torch.cuda.CUDAGraph] = None
+        self._captured_over = None
         lib = _lib.load()
         # Split-K partial products of the QKV, attention-projection and
         # MLP-projection GEMMs, added by the attention and residual+LayerNorm
@@ -241,8 +251,41 @@ class DecodeSession:
                                    self.step.data_ptr(), s), "argmax")
         self.step.add_(1)
 
+    def _weights_key(self):
+        m = self.model
+        return (m.logits_dtype, tuple((k, t.data_ptr()) for k, t in m.weights.items()))
+
+    def matches(self, B: int, t0: int, max_new: int) -> bool:
+        """Whether this session can serve a generation of B sequences with a
+        t0-token prompt and max_new new tokens: same shapes, and the model
+        still holds the weight tensors (and logits dtype) any captured graph
+        was recorded over."""
+        return ((B, t0, max_new) == (self.B, self.t0, self.max_new) and
+                (self._captured_over is None or self._captured_over == self._weights_key()))
+
+    def _capture(self, fn) -> torch.cuda.CUDAGraph:
+        """Capture ``fn`` outside inference mode: torch allocates its graph
+        RNG state on the first capture while no graph is alive, and a graph
+        kept by the session would otherwise leave that state an inference
+        tensor that later captures outside inference mode cannot update."""
+        dev = self.model.device
+        with torch.inference_mode(False):
+            g = torch.cuda.CUDAGraph()
+            side = torch.cuda.Stream(dev)
+            side.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(side):
+                with torch.cuda.graph(g, stream=side):
+                    fn()
+            torch.cuda.current_stream(dev).wait_stream(side)
+        self._captured_over = self._weights_key()
+        return g
+
     def run_greedy(self, use_graph: bool = True) -> torch.Tensor:
-        """Generate ``max_new`` tokens after ``prefill``; returns (B, max_new)."""
+        """Generate ``max_new`` tokens after ``prefill``; returns (B, max_new).
+        The step graph captured by an earlier call on this session is
+        replayed again (the step counter restarts at 0)."""
+        self.step.zero_()
+        self.err.zero_()
         self.greedy_first()
         n = self.max_new - 1
         if n <= 0:
@@ -251,15 +294,22 @@ class DecodeSession:
             for _ in range(n):
                 self.greedy_step()
             return self.hist
-        self.greedy_step()  # eager first step (also loads every kernel)
-        g = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream(self.model.device)
-        side.wait_stream(torch.cuda.current_stream(self.model.device))
-        with torch.cuda.stream(side):
-            with torch.cuda.graph(g, stream=side):
-                self.greedy_step()
-        torch.cuda.current_stream(self.model.device).wait_stream(side)
-        self.graph = g
-        for _ in range(n - 1):
-            g.replay()
+        if self.graph is None:
+            self.greedy_step()  # eager first step (also loads every kernel)
+            self.graph = self._capture(self.greedy_step)
+            n -= 1
+        for _ in range(n):
+            self.graph.replay()
         return self.hist
+
+    def next_logits(self, use_graph: bool = True) -> None:
+        """``step_logits`` for a caller that picks the tokens itself
+        (sampling).  With ``use_graph`` the first call runs eagerly and
+        captures the step; later calls on the session replay it."""
+        if not use_graph:
+            self.step_logits()
+        elif self.graph_logits is not None:
+            self.graph_logits.replay()
+        else:
+            self.step_logits()
+            self.graph_logits = self._capture(self.step_logits)

@@ -54,6 +54,7 @@ class CutileGPT:
         self.logits_dtype = logits_dtype
         self.weights: Dict[str, torch.Tensor] = {}
         self._err = None
+        self._decode_session = None  # the last generate()'s KV cache and step graphs
         if init_weights:
             self._init_weights(seed)
 
@@ -96,6 +97,7 @@ class CutileGPT:
         contiguous, 16-byte aligned buffers.  ``lm_head.weight`` defaults to
         (and, when equal to it, shares storage with) ``wte``."""
         cfg = self.config
+        self._decode_session = None
         out: Dict[str, torch.Tensor] = {}
         for k, v in weights.items():
             if k == "lm_head.weight":
@@ -301,15 +303,24 @@ class CutileGPT:
         if use_cache and T0 + max_new_tokens <= self.config.block_size and B <= 64:
             from .decode import DecodeSession
 
-            sess = DecodeSession(self, B, T0, max_new_tokens)
+            # The last session (its cache, buffers and captured step graphs)
+            # serves the next call of the same shape while the model holds
+            # the same weight tensors.
+            sess = self._decode_session
+            if sess is None or not sess.matches(B, T0, max_new_tokens):
+                self._decode_session = None
+                sess = DecodeSession(self, B, T0, max_new_tokens)
+                self._decode_session = sess
             sess.prefill(idx)
             if top_k == 1:
                 new = sess.run_greedy(use_graph=use_graph)
                 return torch.cat([idx, new], dim=1)
+            sess.step.zero_()
+            sess.err.zero_()
             out = []
             for t in range(max_new_tokens):
                 if t > 0:
-                    sess.step_logits()
+                    sess.next_logits(use_graph=use_graph and max_new_tokens >= 4)
                 nxt = self._sample(sess.logits, temperature, top_k)
                 out.append(nxt)
                 sess.ids.copy_(nxt.view(-1))

@@ -394,6 +394,70 @@ def test_sampled_generate_with_cache_is_reproducible(gpu):
     assert ((a >= 0) & (a < cfg.vocab_size)).all()
 
 
+def test_sampled_generate_graph_equals_eager(gpu):
+    """The sampled path's captured logits step (replayed from the third token
+    on, and again by a second call on the same session) draws exactly the
+    eager path's tokens from the same RNG state."""
+    m, _, cfg = small_model(torch.bfloat16)
+    idx = torch.randint(0, cfg.vocab_size, (3, 5), generator=torch.Generator().manual_seed(8)).to(gpu)
+    outs = []
+    for use_graph in (False, True, True):
+        torch.manual_seed(77)
+        outs.append(m.generate(idx, 9, temperature=0.9, top_k=12, use_graph=use_graph))
+    assert m._decode_session.graph_logits is not None
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
+def test_generate_reuses_session_only_for_same_shape_and_weights(gpu):
+    """A second greedy generate() of the same shape replays the first call's
+    captured step on the same session (new prompt, new stream); new weights
+    (load_weights, or one tensor of the dict replaced) or another shape get
+    a new session.  Every stream equals the oracle's fp32 greedy stream."""
+    m, w, cfg = small_model(torch.float32, n_layer=2, n_head=2, n_embd=64, seed=11)
+    B, T0, n = 3, 5, 10
+    g = torch.Generator().manual_seed(21)
+    p1, p2 = (torch.randint(0, cfg.vocab_size, (B, T0), generator=g) for _ in range(2))
+    out1 = m.generate(p1.to(gpu), n, top_k=1)
+    sess, graph = m._decode_session, m._decode_session.graph
+    assert graph is not None
+    out2 = m.generate(p2.to(gpu), n, top_k=1)
+    assert m._decode_session is sess and sess.graph is graph
+    assert torch.equal(out1.cpu(), R.generate(w, p1, cfg.n_head, n))
+    assert torch.equal(out2.cpu(), R.generate(w, p2, cfg.n_head, n))
+
+    w2 = R.init_weights(2, 2, 64, seed=12)
+    m.load_weights(w2)
+    out3 = m.generate(p1.to(gpu), n, top_k=1)
+    assert m._decode_session is not sess
+    assert torch.equal(out3.cpu(), R.generate(w2, p1, cfg.n_head, n))
+
+    sess3 = m._decode_session
+    key = "h.1.mlp.c_fc.weight"
+    m.weights[key] = m.weights[key].clone()
+    out4 = m.generate(p2.to(gpu), n, top_k=1)
+    assert m._decode_session is not sess3
+    assert torch.equal(out4.cpu(), R.generate(w2, p2, cfg.n_head, n))
+
+    out5 = m.generate(p2[:2].to(gpu), n, top_k=1)
+    assert m._decode_session.B == 2
+    assert torch.equal(out5.cpu(), R.generate(w2, p2[:2], cfg.n_head, n))
+
+    # With the session's graph alive, a graph captured outside inference
+    # mode (as a caller's own) still captures and replays.
+    x = torch.zeros(4, device=gpu)
+    g2 = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(gpu)
+    side.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g2, stream=side):
+            x.add_(1.0)
+    torch.cuda.current_stream(gpu).wait_stream(side)
+    g2.replay()
+    g2.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(x, torch.full((4,), 2.0, device=gpu))
+
+
 def test_decode_session_limits(gpu):
     m, _, cfg = small_model(torch.bfloat16)
     with pytest.raises(ValueError):
