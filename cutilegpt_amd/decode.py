@@ -35,7 +35,9 @@ dtype, t_max = prompt length + new tokens (<= block_size).
 from __future__ import annotations
 
 import ctypes
+import gc
 import math
+import weakref
 from typing import Optional
 
 import torch
@@ -75,7 +77,11 @@ class DecodeSession:
             raise ValueError(f"prompt {t0} + {max_new} new tokens exceeds block_size {cfg.block_size}")
         if B > 64:
             raise ValueError("KV-cache decoding supports at most 64 sequences per batch")
-        self.model = model
+        # A weak reference: the model keeps its last session (generate()), and
+        # a model <-> session cycle would leave dead sessions, with their HIP
+        # graphs, to the cyclic garbage collector, which may run inside a later
+        # stream capture, where destroying a graph is an error.
+        self._model = weakref.ref(model)
         self.B, self.t0, self.max_new = B, t0, max_new
         dev, act = model.device, model.dtype
         D, H, V = cfg.n_embd, cfg.n_head, cfg.vocab_size
@@ -122,6 +128,13 @@ class DecodeSession:
         self.ws = torch.empty(max(ws_max // 4, 4), dtype=torch.float32, device=dev)
         self.ws_bytes = self.ws.numel() * 4
         self.counters = torch.zeros(max(cnt_max, 1), dtype=torch.int32, device=dev)
+
+    @property
+    def model(self):
+        m = self._model()
+        if m is None:
+            raise RuntimeError("the model of this DecodeSession no longer exists")
+        return m
 
     # ----------------------------------------------------------------- prefill
 
@@ -269,14 +282,23 @@ class DecodeSession:
         kept by the session would otherwise leave that state an inference
         tensor that later captures outside inference mode cannot update."""
         dev = self.model.device
-        with torch.inference_mode(False):
-            g = torch.cuda.CUDAGraph()
-            side = torch.cuda.Stream(dev)
-            side.wait_stream(torch.cuda.current_stream(dev))
-            with torch.cuda.stream(side):
-                with torch.cuda.graph(g, stream=side):
-                    fn()
-            torch.cuda.current_stream(dev).wait_stream(side)
+        # Dead objects that hold HIP graphs or memory are freed now, and no
+        # collection runs during the capture (destroying a graph then fails).
+        gc.collect()
+        was_enabled = gc.isenabled()
+        gc.disable()
+        try:
+            with torch.inference_mode(False):
+                g = torch.cuda.CUDAGraph()
+                side = torch.cuda.Stream(dev)
+                side.wait_stream(torch.cuda.current_stream(dev))
+                with torch.cuda.stream(side):
+                    with torch.cuda.graph(g, stream=side):
+                        fn()
+                torch.cuda.current_stream(dev).wait_stream(side)
+        finally:
+            if was_enabled:
+                gc.enable()
         self._captured_over = self._weights_key()
         return g
 

@@ -8,7 +8,9 @@ bf16 ulps of the exact (fp64) result.
 """
 
 import ctypes
+import gc
 import math
+import weakref
 
 import pytest
 import torch
@@ -456,6 +458,24 @@ def test_generate_reuses_session_only_for_same_shape_and_weights(gpu):
     g2.replay()
     torch.cuda.synchronize()
     assert torch.equal(x, torch.full((4,), 2.0, device=gpu))
+
+
+def test_dropped_model_frees_its_session_without_gc(gpu):
+    """A model kept session (with its captured graph) is freed with the model
+    by reference counting alone, not left as cyclic garbage for a collection
+    that could run inside some later stream capture."""
+    m, _, cfg = small_model(torch.bfloat16)
+    idx = torch.randint(0, cfg.vocab_size, (2, 4), generator=torch.Generator().manual_seed(3)).to(gpu)
+    m.generate(idx, 6, top_k=1)
+    sess_ref, model_ref = weakref.ref(m._decode_session), weakref.ref(m)
+    assert sess_ref().graph is not None
+    torch.cuda.synchronize()
+    gc.disable()
+    try:
+        del m
+        assert model_ref() is None and sess_ref() is None
+    finally:
+        gc.enable()
 
 
 def test_decode_session_limits(gpu):
