@@ -274,6 +274,7 @@ class DecodeSession:
         still holds the weight tensors (and logits dtype) any captured graph
         was recorded over."""
         return ((B, t0, max_new) == (self.B, self.t0, self.max_new) and
+                self.logits.dtype == self.model.logits_dtype and
                 (self._captured_over is None or self._captured_over == self._weights_key()))
 
     def _capture(self, fn) -> torch.cuda.CUDAGraph:

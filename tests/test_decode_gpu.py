@@ -444,6 +444,13 @@ def test_generate_reuses_session_only_for_same_shape_and_weights(gpu):
     assert m._decode_session.B == 2
     assert torch.equal(out5.cpu(), R.generate(w2, p2[:2], cfg.n_head, n))
 
+    sess5 = m._decode_session
+    m.logits_dtype = torch.bfloat16
+    out6 = m.generate(p2[:2].to(gpu), n, top_k=1)
+    assert m._decode_session is not sess5 and m._decode_session.logits.dtype == torch.bfloat16
+    assert out6.shape == out5.shape
+    m.logits_dtype = torch.float32
+
     # With the session's graph alive, a graph captured outside inference
     # mode (as a caller's own) still captures and replays.
     x = torch.zeros(4, device=gpu)
