@@ -278,10 +278,18 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // (the compiler cannot prove that a read of one stage buffer does not alias
 // the DMA into another and would otherwise drain the queue before every
 // read).  M0 needs one wait state after its write.
+// M0 is on the clobber list because the statement writes it.  clang warns that
+// it does not save a reserved register around an asm statement (-Winline-asm,
+// once per inlined call); nothing of the compiler's own lives in M0 across one:
+// in the device code of every kernel here the only instructions that name M0
+// are these moves (tests/test_dma_waits.py checks the skinny kernels' code).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma_lds16(u32x4_t desc, uint32_t lds, uint32_t voff, uint32_t soff) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :: "s"(lds), "v"(voff), "s"(desc), "s"(soff) : "memory", "m0");
 }
+#pragma clang diagnostic pop
 #endif
 
 __device__ __forceinline__ void raw_barrier() {

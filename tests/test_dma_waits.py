@@ -9,7 +9,8 @@ every DMA (vmcnt retires in order) without waiting for W.  That holds only
 if exactly n vector-memory loads sit between the last DMA and the wait in
 the emitted code.  The sources arrange it (W is not ``__restrict__``, so its
 loads cannot move across the memory clobbers on either side); this test
-reads the device assembly of every instance and checks it.
+reads the device assembly of every instance and checks it, and that M0,
+which the helper writes from inline assembly, is used by nothing else.
 """
 
 import os
@@ -40,10 +41,26 @@ def _device_asm(tmp_path):
     return out.read_text().splitlines()
 
 
+def _check_m0(lines):
+    """The DMA helper writes M0 from inline assembly (its LDS address); the
+    compiler does not save M0 around it, so no compiler-emitted instruction
+    may use M0: every line that names it must be one of the helper's moves,
+    followed (after its wait state) by the DMA that reads it."""
+    code = [l.strip() for l in lines if l.strip() and not l.strip().startswith(";")]
+    moves = 0
+    for i, line in enumerate(code):
+        if re.search(r"\bm0\b", line):
+            assert line.startswith("s_mov_b32 m0,"), line
+            assert code[i + 1] == "s_nop 0" and code[i + 2].endswith("offen lds"), code[i:i + 3]
+            moves += 1
+    return moves
+
+
 @pytest.mark.skipif(shutil.which("hipcc") is None and not os.path.exists("/opt/rocm/bin/hipcc"),
                     reason="needs hipcc")
 def test_dma_wait_counts_only_the_first_w_round(tmp_path):
     lines = _device_asm(tmp_path)
+    assert _check_m0(lines) > 0
     found = {}
     cur = None
     for line in lines:
