@@ -577,8 +577,11 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4,
               lsum += p[kt][r];
             }
         }
-        const bool settled = m_run[qt] != -INFINITY && lsum <= kOptimisticSum;
-        if (!__all(settled)) {
+        // Every active lane settled: the two compares' lane masks against exec
+        // (__all of their conjunction costs two more VALU instructions).
+        const uint64_t settled = __builtin_amdgcn_ballot_w64(m_run[qt] != -INFINITY) &
+                                 __builtin_amdgcn_ballot_w64(lsum <= kOptimisticSum);
+        if (settled != __builtin_amdgcn_read_exec()) {
           float mloc = -INFINITY;
 #pragma unroll
           for (int kt = 0; kt < 4; ++kt)
