@@ -467,10 +467,14 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4,
   };
 
   f32x4_t o_acc[QT][ND];
-  float m_run[QT], l_run[QT];
+  // nm = minus the running maximum of a query's scaled scores, +inf while the
+  // query has none; l_run = its running normaliser.  Every query sees key 0
+  // (Tk >= Tq, checked by the entry point), so the first key block gives
+  // every lane a finite maximum unless its scores are not finite numbers.
+  float nm[QT], l_run[QT];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    m_run[qt] = -INFINITY;
+    nm[qt] = INFINITY;
     l_run[qt] = 0.f;
 #pragma unroll
     for (int dt = 0; dt < ND; ++dt) o_acc[qt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -556,32 +560,30 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4,
       // P against the running maximum as it stands, before the block's own
       // maximum is known.  A lane whose 16 values sum to at most 2^7 has none
       // above 2^7, i.e. its scores sit at least 1 (log2 units) below the lazy
-      // threshold m_run + kLazyLog2, so the rule below keeps m_run for its
-      // query and these values are the final ones.  Only when some lane of the
-      // wave fails that (a NaN sum fails it too) or has no maximum yet is the
-      // block maximum taken and the rule applied; lanes whose maximum moves
-      // recompute their values.  The results equal those of always applying
-      // the rule first, bit for bit, and the common block skips the maximum.
+      // threshold (running maximum + kLazyLog2), so the rule below keeps the
+      // maximum for its query and these values are the final ones.  Only when
+      // some lane of the wave fails that (a NaN sum fails it too, and so does
+      // a query with no maximum yet) is the block maximum taken and the rule
+      // applied; lanes whose maximum moves recompute their values.  The
+      // results equal those of always applying the rule first, bit for bit,
+      // and the common block skips the maximum.
       constexpr float kOptimisticSum = 128.0f;
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) {
         float p[4][4];
         float lsum = 0.f;
-        {
-          const float neg_m = m_run[qt] == -INFINITY ? 0.f : -m_run[qt];
 #pragma unroll
-          for (int kt = 0; kt < 4; ++kt)
+        for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              p[kt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qt][kt][r], scale_log2, neg_m));
-              lsum += p[kt][r];
-            }
-        }
-        // Every active lane settled: the two compares' lane masks against exec
-        // (__all of their conjunction costs two more VALU instructions).
-        const uint64_t settled = __builtin_amdgcn_ballot_w64(m_run[qt] != -INFINITY) &
-                                 __builtin_amdgcn_ballot_w64(lsum <= kOptimisticSum);
-        if (settled != __builtin_amdgcn_read_exec()) {
+          for (int r = 0; r < 4; ++r) {
+            p[kt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qt][kt][r], scale_log2, nm[qt]));
+            lsum += p[kt][r];
+          }
+        // Every active lane settled: the compare's lane mask against exec (__all
+        // would take two more VALU instructions).  A query with no maximum yet
+        // (nm = +inf) sums to +inf or NaN and fails the test.
+        if (__builtin_amdgcn_ballot_w64(lsum <= kOptimisticSum) != __builtin_amdgcn_read_exec()) {
+          const float m_old = -nm[qt];  // -inf while the query has no maximum
           float mloc = -INFINITY;
 #pragma unroll
           for (int kt = 0; kt < 4; ++kt)
@@ -589,25 +591,24 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4,
             for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, s[qt][kt][r]);
           mloc = column_max(mloc);
           const float mblk = mloc * scale_log2;
-          const bool grow = mblk > m_run[qt] + kLazyLog2;
+          const bool grow = mblk > m_old + kLazyLog2;
           if (__any(grow)) {
-            const float m_new = grow ? mblk : m_run[qt];
-            const float alpha = grow ? __builtin_amdgcn_exp2f(m_run[qt] - m_new) : 1.0f;
-            m_run[qt] = m_new;
+            const float m_new = grow ? mblk : m_old;
+            const float alpha = grow ? __builtin_amdgcn_exp2f(m_old - m_new) : 1.0f;
+            nm[qt] = m_new == -INFINITY ? INFINITY : -m_new;
             l_run[qt] *= alpha;
 #pragma unroll
             for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
               for (int r = 0; r < 4; ++r) o_acc[qt][dt][r] *= alpha;
             if (grow) {
-              const float neg_m = m_run[qt] == -INFINITY ? 0.f : -m_run[qt];
               lsum = 0.f;
 #pragma unroll
               for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                   p[kt][r] =
-                      __builtin_amdgcn_exp2f(__builtin_fmaf(s[qt][kt][r], scale_log2, neg_m));
+                      __builtin_amdgcn_exp2f(__builtin_fmaf(s[qt][kt][r], scale_log2, nm[qt]));
                   lsum += p[kt][r];
                 }
             }
