@@ -268,7 +268,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
         mloc = column_max(mloc);
         const float mblk = mloc * scale_log2;  // scale > 0: max commutes
         const bool grow = mblk > m_run[qt] + kLazyLog2;
-        if (__any(grow)) {
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
           const float m_new = grow ? mblk : m_run[qt];
           const float alpha = grow ? __builtin_amdgcn_exp2f(m_run[qt] - m_new) : 1.0f;
           m_run[qt] = m_new;
@@ -592,7 +592,7 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4,
           mloc = column_max(mloc);
           const float mblk = mloc * scale_log2;
           const bool grow = mblk > m_old + kLazyLog2;
-          if (__any(grow)) {
+          if (__builtin_amdgcn_ballot_w64(grow) != 0) {
             const float m_new = grow ? mblk : m_old;
             const float alpha = grow ? __builtin_amdgcn_exp2f(m_old - m_new) : 1.0f;
             nm[qt] = m_new == -INFINITY ? INFINITY : -m_new;
